@@ -1,0 +1,115 @@
+/*
+ * tq4_decode.h -- C ABI of the MI355X (gfx950) TurboQuant `turboquant_4bit_nc`
+ * decode path: Stage1 split-KV attention over the 4-bit paged cache, the Stage2
+ * split reduction, and the query-rotation / pair-LUT prologue of a full step.
+ *
+ * All pointers are device pointers; all calls are asynchronous on `stream` and
+ * allocate nothing.  Every entry point returns 0 on success, otherwise a
+ * nonzero code (TQ4_E_*, or the HIP error of a failed launch) and records a
+ * message readable with tq4_last_error() on the calling thread.  Nothing throws.
+ *
+ * Shapes (row-major, contiguous):
+ *   q_rot       float32 [B, Hq, D]            (D == 128)
+ *   kv_cache    uint8   [num_blocks, block_size, Hk, slot]  slot = 134 at D=128,
+ *               physical block stride = cache_block_stride bytes
+ *   block_table int32   [B, max_blocks_per_seq]
+ *   seq_lens    int32   [B]
+ *   pair_lut    float32 [256, 2]              row lo*16+hi = (c[lo], c[hi])
+ *   mid_o       float32 [B, Hq, S, D + 1]     S = num_kv_splits; [.., D] holds LSE
+ *   out         [B, Hq, D] in out_dtype; lse float32 [B, Hq]
+ */
+#ifndef TQ4_DECODE_H
+#define TQ4_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *tq4_stream_t; /* same type as hipStream_t */
+
+enum tq4_layout { TQ4_LAYOUT_SOA = 0, TQ4_LAYOUT_AOS = 1 };
+enum tq4_dtype { TQ4_F32 = 0, TQ4_BF16 = 1, TQ4_F16 = 2 };
+enum tq4_kernel { TQ4_KERNEL_AUTO = 0, TQ4_KERNEL_SIMPLE = 1, TQ4_KERNEL_MFMA = 2 };
+enum tq4_status {
+    TQ4_OK = 0,
+    TQ4_E_INVALID = 1,     /* a shape, pointer or alignment argument is invalid   */
+    TQ4_E_UNSUPPORTED = 2  /* valid, but outside the shapes these kernels cover   */
+};
+
+/*
+ * Stage1: per (sequence b, kv-head, split) partial attention.  Split s covers
+ * tokens [s*L, min((s+1)*L, seq_lens[b])) with L = ceil(seq_lens[b] / S); an
+ * empty split leaves its mid_o rows untouched.  mid_o[b,h,s,:D] = sum p v / sum p,
+ * mid_o[b,h,s,D] = natural-log LSE of the split's scores
+ *   score_t = attn_scale * n_t * sum_d q[d] * c[idx_td]
+ * (SoA: n_t is the stored folded norm; AoS: raw norm / ||c[idx_t]||).
+ * Replaces: launch_tq4_v2_stage1  baseline/triton_v2.py:569-706 (SoA),
+ *           launch_soa_v1_stage1  baseline/triton_v1.py:145-203 (SoA),
+ *           launch_aos_v1_stage1  baseline/triton_v1.py:90-142  (AoS),
+ *           tq4_cuda_vN           cuda/tq4_cuda_v9.cu:276-306, cuda/tq4_cuda_v9_bind.cpp:3-8.
+ * The grid depends only on (B, Hk, S), never on seq_lens values.
+ */
+int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+               const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,
+               int Hk, int D, int block_size, int max_blocks_per_seq,
+               int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+               tq4_stream_t stream);
+
+/* Same as tq4_stage1 with an explicit kernel choice (TQ4_KERNEL_*): SIMPLE is the
+ * plain-VALU kernel (any GQA group up to 16), MFMA the matrix-core kernel (GQA
+ * group 4 or 8, block_size a multiple of 16).  AUTO picks MFMA when it applies.
+ * Replaces: the per-version entry points tq4_cuda_v1 .. tq4_cuda_v9 (cuda/tq4_cuda_vN_bind.cpp). */
+int tq4_stage1_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+                  const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,
+                  int Hk, int D, int block_size, int max_blocks_per_seq,
+                  int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+                  int kernel, tq4_stream_t stream);
+
+/*
+ * Stage2: merge the non-empty splits of every (b, h):
+ *   M = max lse_s, w_s = exp(lse_s - M), out = sum w_s o_s / sum w_s, lse = M + ln sum w_s.
+ * Replaces: launch_stage2 baseline/stage2.py:58-81 (kernel :8-55);
+ *           tq4_cuda_v7_stage2 cuda/tq4_cuda_v7.cu:56-76 (which merges all splits).
+ */
+int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_dtype,
+               float *lse, int B, int Hq, int D, int num_kv_splits, tq4_stream_t stream);
+
+/*
+ * q_rot[r, :] = float(query[r, :]) @ rot_t  for r < rows (query in query_dtype).
+ * Replaces: `q_rot = (query.float() @ PiT)` reference/soa_decode_v1.py:532-538.
+ */
+int tq4_rotate_query(const void *query, int query_dtype, const float *rot_t, float *q_rot,
+                     int rows, int D, tq4_stream_t stream);
+
+/* pair_lut[lo*n + hi] = (c[lo], c[hi]).  Replaces: build_pair_lut baseline/common.py:232-257. */
+int tq4_build_pair_lut(const float *centroids, float *pair_lut, int n_centroids,
+                       tq4_stream_t stream);
+
+/*
+ * Full decode step: rotate query into q_rot_ws, build the pair LUT into
+ * pair_lut_ws (512 floats), Stage1 into mid_o, Stage2 into out / lse.
+ * Replaces: tq4_cuda_v7_full cuda/tq4_cuda_v7.cu:78-84 plus the q rotation of
+ *           triton_turboquant_decode_attention reference/soa_decode_v1.py:485-643.
+ */
+int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
+                    const float *centroids, const uint8_t *kv_cache,
+                    const int32_t *block_table, const int32_t *seq_lens, float *q_rot_ws,
+                    float *pair_lut_ws, float *mid_o, void *out, int out_dtype, float *lse,
+                    int B, int Hq, int Hk, int D, int block_size, int max_blocks_per_seq,
+                    int64_t cache_block_stride, int num_kv_splits, int layout,
+                    float attn_scale, tq4_stream_t stream);
+
+/* Message of the last failed call on this thread ("" when none).
+ * Replaces: the TORCH_CHECK messages of cuda/tq4_cuda_v1.cu:468-499. */
+const char *tq4_last_error(void);
+
+/* ABI version of this library (major*100 + minor). */
+int tq4_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ4_DECODE_H */

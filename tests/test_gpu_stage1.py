@@ -1,0 +1,132 @@
+"""Stage1 parity on the GPU: HIP kernels (through the C ABI) vs the oracle.
+
+Bar: max-abs <= 1e-4 on mid_o (outputs and LSE, fp32), identical untouched-split
+pattern (mid_o is pre-filled with NaN; empty splits must stay NaN).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev
+from oracle import native
+from tq4_decode import ops, workloads
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def run(w, dev, kernel, layout="soa", cache=None):
+    cache = w.kv_cache if cache is None else cache
+    mid = torch.full((w.batch, w.num_q_heads, w.num_kv_splits, 129), float("nan"), device=dev)
+    ops.stage1(to_dev(w.q_rot, dev), to_dev(cache, dev), to_dev(w.block_table, dev),
+               to_dev(w.seq_lens, dev), to_dev(w.pair_lut, dev), mid, layout=layout, kernel=kernel)
+    torch.cuda.synchronize()
+    return mid.cpu().numpy()
+
+
+def oracle(w, layout="soa", cache=None):
+    cache = w.kv_cache if cache is None else cache
+    return native.stage1(w.q_rot, cache, w.block_table, w.seq_lens, w.centroids, w.num_kv_splits,
+                         num_kv_heads=w.num_kv_heads, block_size=w.block_size,
+                         is_aos=layout == "aos")
+
+
+def assert_parity(got, ref, tol=TOL):
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "untouched-split pattern differs"
+    err = np.nanmax(np.abs(got - ref))
+    print(f"max-abs {err:.3e}")
+    assert err <= tol, f"max-abs {err} > {tol}"
+
+
+@pytest.mark.parametrize("kernel", ["simple", "mfma"])
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_store_fixture_b2_ctx256(config1, dev, kernel, layout):
+    f = config1
+    w = workloads.Workload("config1", f["q_rot"], f[f"cache_{layout}"], f["block_table"],
+                           f["seq_lens"], f["centroids"], int(f["num_kv_splits"]),
+                           int(f["num_kv_heads"]))
+    got = run(w, dev, kernel, layout)
+    assert_parity(got, f[f"mid_{layout}"])
+
+
+@pytest.mark.parametrize("kernel", ["simple", "mfma"])
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_ragged_with_empty_and_partial_splits(dev, kernel, layout):
+    w = workloads.small(101, 6, [1, 3, 17, 100, 257, 999], 32)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, 8) if layout == "aos" else None
+    assert_parity(run(w, dev, kernel, layout, cache), oracle(w, layout, cache))
+
+
+@pytest.mark.parametrize("kernel,group", [("simple", 1), ("simple", 2), ("simple", 4),
+                                          ("simple", 8), ("simple", 16), ("mfma", 4),
+                                          ("mfma", 8)])
+def test_gqa_groups(dev, kernel, group):
+    hk = 4
+    w = workloads.small(102, 3, [77, 300, 1024], 7, num_q_heads=hk * group, num_kv_heads=hk)
+    assert_parity(run(w, dev, kernel), oracle(w))
+
+
+@pytest.mark.parametrize("kernel", ["simple", "mfma"])
+@pytest.mark.parametrize("bs", [32, 64])
+def test_larger_kv_blocks(dev, kernel, bs):
+    w = workloads.small(103, 3, [130, 511, 64], 5, block_size=bs)
+    for layout in ("soa", "aos"):
+        cache = workloads.soa_to_aos(w.kv_cache, w.centroids, 8, block_size=bs) if layout == "aos" else None
+        assert_parity(run(w, dev, kernel, layout, cache), oracle(w, layout, cache))
+
+
+def test_large_scores_rescale_path(dev):
+    """q scaled x40: scores span tens of units, so the running max moves often."""
+    w = workloads.small(104, 2, [640, 333], 3)
+    w.q_rot = (w.q_rot * 40).astype(np.float32)
+    assert_parity(run(w, dev, "mfma"), oracle(w))
+    assert_parity(run(w, dev, "simple"), oracle(w))
+
+
+@pytest.fixture(scope="module")
+def qwen():
+    w = workloads.qwen3_4b_b64_ctx4096()
+    return w, workloads.soa_to_aos(w.kv_cache, w.centroids, 8)
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_qwen3_4b_b64_ctx4096_full_size(qwen, dev, layout):
+    w, aos = qwen
+    cache = aos if layout == "aos" else None
+    ref = oracle(w, layout, cache)
+    assert_parity(run(w, dev, "auto", layout, cache), ref)
+
+
+def test_mfma_and_simple_agree_full_size(qwen, dev):
+    w, _ = qwen
+    a, b = run(w, dev, "mfma"), run(w, dev, "simple")
+    assert_parity(a, b, 2e-5)
+
+
+def test_ragged_b64_full_size(dev):
+    w = workloads.ragged_b64()
+    assert_parity(run(w, dev, "auto"), oracle(w))
+
+
+def test_gqa8_b8_ctx32768_full_size(dev):
+    w = workloads.gqa8_b8_ctx32768()
+    assert_parity(run(w, dev, "auto"), oracle(w))
+
+
+def test_reference_call_shapes(qwen, dev):
+    w, aos = qwen
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    q, bt, sl, cents = t(w.q_rot), t(w.block_table), t(w.seq_lens), t(w.centroids)
+    soa_c, aos_c = t(w.kv_cache), t(aos)
+    lut = ops.pair_lut_device(cents)
+    assert torch.equal(lut.cpu(), torch.from_numpy(w.pair_lut))
+    mid_v2 = ops.launch_tq4_v2_stage1(q, soa_c, bt, sl, cents, lut)  # allocates mid_o
+    mid_ext = torch.empty_like(mid_v2)
+    ops.ext.tq4_cuda_v9(q, soa_c, bt, sl, cents, mid_ext)
+    mid_aos = torch.empty_like(mid_v2)
+    ops.launch_aos_v1_stage1(q, aos_c, bt, sl, cents, mid_aos)
+    torch.cuda.synchronize()
+    ref = oracle(w)
+    assert_parity(mid_v2.cpu().numpy(), ref)
+    assert torch.equal(mid_v2, mid_ext)
+    assert_parity(mid_aos.cpu().numpy(), oracle(w, "aos", aos))

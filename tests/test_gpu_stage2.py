@@ -1,0 +1,98 @@
+"""Stage2 and full-decode parity on the GPU."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev
+from oracle import native, stage1 as ostage
+from tq4_decode import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _mid_on_gpu(w, dev):
+    mid = torch.full((w.batch, w.num_q_heads, w.num_kv_splits, 129), float("nan"), device=dev)
+    ops.stage1(to_dev(w.q_rot, dev), to_dev(w.kv_cache, dev), to_dev(w.block_table, dev),
+               to_dev(w.seq_lens, dev), to_dev(w.pair_lut, dev), mid)
+    return mid
+
+
+@pytest.mark.parametrize("lens,splits", [([1, 3, 17, 100, 257, 999], 32), ([4096, 4095], 32),
+                                         ([5000, 70], 64), ([64], 1)])
+def test_stage2_matches_oracle_and_skips_empty_splits(dev, lens, splits):
+    w = workloads.small(201, len(lens), lens, splits)
+    mid = _mid_on_gpu(w, dev)  # empty splits hold NaN: merging one would poison the output
+    out, lse = ops.stage2(mid, to_dev(w.seq_lens, dev))
+    torch.cuda.synchronize()
+    ro, rl = native.stage2(mid.cpu().numpy(), w.seq_lens)
+    assert np.isfinite(out.cpu().numpy()).all()
+    assert np.abs(out.cpu().numpy() - ro).max() <= 1e-5
+    assert np.abs(lse.cpu().numpy() - rl).max() <= 1e-5
+    fo, fl = ostage.attention_reference(w.q_rot, w.kv_cache, w.block_table, w.seq_lens,
+                                        w.centroids, num_kv_heads=8)
+    assert np.abs(out.cpu().numpy() - fo).max() <= 1e-4
+    assert np.abs(lse.cpu().numpy() - fl).max() <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_stage2_output_dtypes(dev, dtype):
+    w = workloads.small(202, 3, [300, 45, 1000], 16)
+    mid = _mid_on_gpu(w, dev)
+    ref, _ = ops.stage2(mid, to_dev(w.seq_lens, dev))
+    got, _ = ops.stage2(mid, to_dev(w.seq_lens, dev), out_dtype=dtype)
+    assert torch.equal(got, ref.to(dtype))
+
+
+def test_reference_stage2_call_shapes(dev):
+    w = workloads.small(203, 2, [4096, 4096], 32)
+    sl = to_dev(w.seq_lens, dev)
+    mid = _mid_on_gpu(w, dev)
+    out = torch.empty(2, 32, 128, device=dev)
+    lse = torch.empty(2, 32, device=dev)
+    ops.launch_stage2(mid, sl, out, lse)
+    out7 = torch.empty_like(out)
+    lse7 = torch.empty_like(lse)
+    ops.ext.tq4_cuda_v7_stage2(mid, out7, lse7, sl)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out7) and torch.equal(lse, lse7)
+
+
+def test_rotate_query_matches_fp64(dev):
+    rng = np.random.default_rng(204)
+    query = rng.standard_normal((40, 3, 128)).astype(np.float16)
+    rot = workloads.random_orthogonal(rng, 128)
+    got = ops.rotate_query(to_dev(query, dev), to_dev(rot, dev)).cpu().numpy()
+    ref = query.astype(np.float64) @ rot.astype(np.float64)
+    assert np.abs(got - ref).max() <= 2e-5
+
+
+def test_full_b256_ctx2048_bf16(dev):
+    w = workloads.full_b256_ctx2048()
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    out, lse = ops.full_decode(t(w.query), t(w.rotation_t), t(w.kv_cache), t(w.block_table),
+                               t(w.seq_lens), t(w.centroids), w.num_kv_splits,
+                               out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    q_rot = (w.query.astype(np.float64) @ w.rotation_t.astype(np.float64)).astype(np.float32)
+    mid = native.stage1(q_rot, w.kv_cache, w.block_table, w.seq_lens, w.centroids,
+                        w.num_kv_splits, num_kv_heads=8)
+    ro, rl = native.stage2(mid, w.seq_lens)
+    err = np.abs(out.float().cpu().numpy() - ro).max()
+    print(f"full decode bf16 max-abs {err:.3e}")
+    assert err <= 1e-3
+    assert np.abs(lse.cpu().numpy() - rl).max() <= 1e-4
+
+
+def test_full_decode_reference_ext_shape(dev):
+    w = workloads.small(205, 4, [4096, 2000, 1, 77], 32)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    mid = torch.empty(4, 32, 32, 129, device=dev)
+    out = torch.empty(4, 32, 128, device=dev)
+    lse = torch.empty(4, 32, device=dev)
+    ops.ext.tq4_cuda_v7_full(t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens),
+                             t(w.centroids), mid, out, lse)
+    torch.cuda.synchronize()
+    fo, fl = ostage.attention_reference(w.q_rot, w.kv_cache, w.block_table, w.seq_lens,
+                                        w.centroids, num_kv_heads=8)
+    assert np.abs(out.cpu().numpy() - fo).max() <= 1e-4
+    assert np.abs(lse.cpu().numpy() - fl).max() <= 1e-4

@@ -1,0 +1,257 @@
+// C ABI of the gfx950 TurboQuant 4-bit decode path (declared in include/tq4_decode.h).
+//
+// Argument checks mirror the TORCH_CHECKs of the reference CUDA entry points
+// (cuda/tq4_cuda_v1.cu:468-499, cuda/tq4_cuda_v7.cu:58-68) and the launcher asserts of
+// baseline/triton_v2.py:594-607, but report through a return code and a thread-local
+// message instead of throwing.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/tq4_decode.h"
+#include "stage1_mfma.h"
+#include "stage1_simple.h"
+#include "stage2.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = '\0';
+    return TQ4_OK;
+}
+
+int launch_status(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail((int)e, "%s launch failed: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+struct Stage1Args {
+    const float *q_rot;
+    const uint8_t *cache;
+    const int32_t *bt;
+    const int32_t *seq_lens;
+    const float *lut;
+    float *mid_o;
+    int B, Hq, Hk, D, bs, max_blocks;
+    int64_t stride;
+    int S, layout;
+    float scale;
+};
+
+int check_stage1(const Stage1Args &a) {
+    if (!a.q_rot || !a.cache || !a.bt || !a.seq_lens || !a.lut || !a.mid_o)
+        return fail(TQ4_E_INVALID, "tq4_stage1: null pointer argument");
+    if (a.B <= 0 || a.Hq <= 0 || a.Hk <= 0 || a.S <= 0 || a.bs <= 0 || a.max_blocks <= 0)
+        return fail(TQ4_E_INVALID, "tq4_stage1: B, Hq, Hk, num_kv_splits, block_size and "
+                                   "max_blocks_per_seq must be positive");
+    if (a.Hq % a.Hk)
+        return fail(TQ4_E_INVALID, "tq4_stage1: Hq (%d) must be a multiple of Hk (%d)", a.Hq, a.Hk);
+    if (a.D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: head_dim %d unsupported (kernels are built for 128)", a.D);
+    if (a.layout != TQ4_LAYOUT_SOA && a.layout != TQ4_LAYOUT_AOS)
+        return fail(TQ4_E_INVALID, "tq4_stage1: layout must be 0 (SoA) or 1 (AoS)");
+    const int64_t min_stride = (int64_t)a.bs * a.Hk * tq4::kAosSlot;
+    if (a.stride < min_stride || a.stride % 2)
+        return fail(TQ4_E_INVALID, "tq4_stage1: requires cache [blocks,%d,%d,134]: block stride %lld < %lld",
+                    a.bs, a.Hk, (long long)a.stride, (long long)min_stride);
+    if (!aligned(a.cache, 16) || !aligned(a.q_rot, 16) || !aligned(a.mid_o, 4))
+        return fail(TQ4_E_INVALID, "tq4_stage1: kv_cache and q_rot must be 16-byte aligned");
+    if (!(a.scale > 0.f) || a.scale != a.scale)
+        return fail(TQ4_E_INVALID, "tq4_stage1: attn_scale must be positive");
+    return TQ4_OK;
+}
+
+template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t st) {
+    const dim3 grid(a.S, a.Hk, a.B);
+    hipLaunchKernelGGL((tq4::stage1_simple_kernel<LAYOUT, G>), grid, dim3(tq4::kWave), 0, st,
+                       a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk, a.bs,
+                       a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
+}
+
+template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_t st) {
+    const dim3 grid(a.S, a.Hk, a.B);
+    hipLaunchKernelGGL((tq4::stage1_mfma_kernel<LAYOUT, NSET>), grid, dim3(tq4::kWave), 0, st,
+                       a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk, a.bs,
+                       a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
+}
+
+template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
+    switch (a.Hq / a.Hk) {
+    case 1: launch_simple<LAYOUT, 1>(a, st); break;
+    case 2: launch_simple<LAYOUT, 2>(a, st); break;
+    case 4: launch_simple<LAYOUT, 4>(a, st); break;
+    case 8: launch_simple<LAYOUT, 8>(a, st); break;
+    case 16: launch_simple<LAYOUT, 16>(a, st); break;
+    default:
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: GQA group %d unsupported (1, 2, 4, 8, 16)",
+                    a.Hq / a.Hk);
+    }
+    return launch_status("stage1_simple");
+}
+
+bool mfma_applies(const Stage1Args &a) {
+    const int g = a.Hq / a.Hk;
+    return (g == 4 || g == 8) && a.bs % 16 == 0 && a.stride % 16 == 0;
+}
+
+template <int LAYOUT> int dispatch_mfma(const Stage1Args &a, hipStream_t st) {
+    if (!mfma_applies(a))
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: MFMA kernel needs GQA group 4 or 8, "
+                                       "block_size %% 16 == 0 and a 16-byte block stride");
+    if (a.Hq / a.Hk == 4)
+        launch_mfma<LAYOUT, 1>(a, st);
+    else
+        launch_mfma<LAYOUT, 2>(a, st);
+    return launch_status("stage1_mfma");
+}
+
+int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
+    int rc = check_stage1(a);
+    if (rc)
+        return rc;
+    if (kernel == TQ4_KERNEL_AUTO)
+        kernel = mfma_applies(a) ? TQ4_KERNEL_MFMA : TQ4_KERNEL_SIMPLE;
+    if (kernel == TQ4_KERNEL_MFMA)
+        return a.layout == TQ4_LAYOUT_SOA ? dispatch_mfma<0>(a, st) : dispatch_mfma<1>(a, st);
+    if (kernel == TQ4_KERNEL_SIMPLE)
+        return a.layout == TQ4_LAYOUT_SOA ? dispatch_simple<0>(a, st) : dispatch_simple<1>(a, st);
+    return fail(TQ4_E_INVALID, "tq4_stage1_ex: unknown kernel id %d", kernel);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tq4_abi_version(void) { return 100; }
+
+const char *tq4_last_error(void) { return g_err; }
+
+int tq4_stage1_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+                  const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,
+                  int Hk, int D, int block_size, int max_blocks_per_seq,
+                  int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+                  int kernel, tq4_stream_t stream) {
+    const Stage1Args a{q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o, B, Hq, Hk, D,
+                       block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits,
+                       layout, attn_scale};
+    return run_stage1(a, kernel, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+               const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,
+               int Hk, int D, int block_size, int max_blocks_per_seq,
+               int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+               tq4_stream_t stream) {
+    return tq4_stage1_ex(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o, B, Hq, Hk, D,
+                         block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits,
+                         layout, attn_scale, TQ4_KERNEL_AUTO, stream);
+}
+
+int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_dtype,
+               float *lse, int B, int Hq, int D, int num_kv_splits, tq4_stream_t stream) {
+    if (!mid_o || !seq_lens || !out || !lse)
+        return fail(TQ4_E_INVALID, "tq4_stage2: null pointer argument");
+    if (B <= 0 || Hq <= 0 || num_kv_splits <= 0)
+        return fail(TQ4_E_INVALID, "tq4_stage2: B, Hq and num_kv_splits must be positive");
+    if (D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage2: head_dim %d unsupported (128)", D);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(Hq, B);
+    switch (out_dtype) {
+    case TQ4_F32:
+        hipLaunchKernelGGL(tq4::stage2_kernel<float>, grid, dim3(tq4::kWave), 0, st, mid_o,
+                           seq_lens, static_cast<float *>(out), lse, Hq, num_kv_splits);
+        break;
+    case TQ4_BF16:
+        hipLaunchKernelGGL(tq4::stage2_kernel<__bf16>, grid, dim3(tq4::kWave), 0, st, mid_o,
+                           seq_lens, static_cast<__bf16 *>(out), lse, Hq, num_kv_splits);
+        break;
+    case TQ4_F16:
+        hipLaunchKernelGGL(tq4::stage2_kernel<_Float16>, grid, dim3(tq4::kWave), 0, st, mid_o,
+                           seq_lens, static_cast<_Float16 *>(out), lse, Hq, num_kv_splits);
+        break;
+    default:
+        return fail(TQ4_E_INVALID, "tq4_stage2: out_dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
+    }
+    return launch_status("stage2");
+}
+
+int tq4_rotate_query(const void *query, int query_dtype, const float *rot_t, float *q_rot,
+                     int rows, int D, tq4_stream_t stream) {
+    if (!query || !rot_t || !q_rot)
+        return fail(TQ4_E_INVALID, "tq4_rotate_query: null pointer argument");
+    if (rows <= 0)
+        return fail(TQ4_E_INVALID, "tq4_rotate_query: rows must be positive");
+    if (D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_rotate_query: head_dim %d unsupported (128)", D);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid((rows + tq4::kRotRows - 1) / tq4::kRotRows);
+    switch (query_dtype) {
+    case TQ4_F32:
+        hipLaunchKernelGGL(tq4::rotate_query_kernel<float>, grid, dim3(tq4::kHeadDim), 0, st,
+                           static_cast<const float *>(query), rot_t, q_rot, rows);
+        break;
+    case TQ4_BF16:
+        hipLaunchKernelGGL(tq4::rotate_query_kernel<__bf16>, grid, dim3(tq4::kHeadDim), 0, st,
+                           static_cast<const __bf16 *>(query), rot_t, q_rot, rows);
+        break;
+    case TQ4_F16:
+        hipLaunchKernelGGL(tq4::rotate_query_kernel<_Float16>, grid, dim3(tq4::kHeadDim), 0, st,
+                           static_cast<const _Float16 *>(query), rot_t, q_rot, rows);
+        break;
+    default:
+        return fail(TQ4_E_INVALID, "tq4_rotate_query: query_dtype must be 0, 1 or 2");
+    }
+    return launch_status("rotate_query");
+}
+
+int tq4_build_pair_lut(const float *centroids, float *pair_lut, int n_centroids,
+                       tq4_stream_t stream) {
+    if (!centroids || !pair_lut)
+        return fail(TQ4_E_INVALID, "tq4_build_pair_lut: null pointer argument");
+    if (n_centroids != 16)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_build_pair_lut: 16 centroids (4-bit keys) expected, got %d",
+                    n_centroids);
+    hipLaunchKernelGGL(tq4::pair_lut_kernel, dim3(1), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), centroids, pair_lut, n_centroids);
+    return launch_status("pair_lut");
+}
+
+int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
+                    const float *centroids, const uint8_t *kv_cache,
+                    const int32_t *block_table, const int32_t *seq_lens, float *q_rot_ws,
+                    float *pair_lut_ws, float *mid_o, void *out, int out_dtype, float *lse,
+                    int B, int Hq, int Hk, int D, int block_size, int max_blocks_per_seq,
+                    int64_t cache_block_stride, int num_kv_splits, int layout,
+                    float attn_scale, tq4_stream_t stream) {
+    int rc = tq4_rotate_query(query, query_dtype, rot_t, q_rot_ws, B * Hq, D, stream);
+    if (rc)
+        return rc;
+    rc = tq4_build_pair_lut(centroids, pair_lut_ws, 16, stream);
+    if (rc)
+        return rc;
+    rc = tq4_stage1(q_rot_ws, kv_cache, block_table, seq_lens, pair_lut_ws, mid_o, B, Hq, Hk, D,
+                    block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
+                    attn_scale, stream);
+    if (rc)
+        return rc;
+    return tq4_stage2(mid_o, seq_lens, out, out_dtype, lse, B, Hq, D, num_kv_splits, stream);
+}
+
+}  // extern "C"

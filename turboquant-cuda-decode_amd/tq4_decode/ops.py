@@ -1,0 +1,256 @@
+"""Torch-facing launchers over the C ABI, with the reference harness's call shapes.
+
+Every launcher validates its tensors with the reference's messages
+(``cuda/tq4_cuda_v1.cu:468-499``), then calls the HIP library on torch's current
+stream of the tensors' device.  Nothing here computes on the host: when the
+library is missing, ``_lib.load`` raises.
+
+Reference call shapes kept here:
+
+* ``launch_tq4_v2_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, pair_lut, mid_o=None)``
+  -- ``baseline/triton_v2.py:569-706`` (SoA; allocates ``mid_o`` when None)
+* ``launch_soa_v1_stage1`` / ``launch_aos_v1_stage1(q_rot, kv_cache, block_table, seq_lens,
+  centroids, mid_o)`` -- ``baseline/triton_v1.py:90-203``
+* ``launch_stage2(mid_o, seq_lens, output, lse)`` -- ``baseline/stage2.py:58-81``
+* ``ext`` -- object with the CUDA-extension names ``tq4_cuda_v1 .. tq4_cuda_v9``,
+  ``tq4_cuda_v7_stage1 / _stage2 / _full`` (``cuda/tq4_cuda_v7_bind.cpp:3-20``), so
+  ``cuda_ext = tq4_decode.ext`` drops into ``benchmarks/stage1.py`` / ``full_decode.py``.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .layout import AOS, LAYOUTS, SOA, slot_bytes
+
+KERNELS = {"auto": 0, "simple": 1, "mfma": 2}
+DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+HEAD_DIM = 128
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    _require(t.is_cuda, f"{name} must be CUDA")
+    _require(t.dtype == dtype, f"{name} must be {str(dtype).replace('torch.', '')}")
+    _require(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def _layout_id(layout) -> int:
+    if isinstance(layout, str):
+        _require(layout in LAYOUTS, f"layout must be one of {sorted(LAYOUTS)}")
+        return LAYOUTS[layout]
+    _require(layout in (SOA, AOS), "layout must be 0 (SoA) or 1 (AoS)")
+    return int(layout)
+
+
+def pair_lut_device(centroids: torch.Tensor) -> torch.Tensor:
+    """Pair LUT ``[n*n, 2]`` built on the centroids' device (``baseline/common.py:232-257``)."""
+    _check_tensor(centroids, "centroids", torch.float32)
+    _require(centroids.numel() == 16, "4-bit path requires 16 centroids")
+    lut = torch.empty(256, 2, dtype=torch.float32, device=centroids.device)
+    _lib.check(_lib.load().tq4_build_pair_lut(centroids.data_ptr(), lut.data_ptr(), 16,
+                                              _stream(centroids.device)), "tq4_build_pair_lut")
+    return lut
+
+
+def stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o=None, *, num_kv_splits=None,
+           layout="soa", attn_scale=None, kernel="auto"):
+    """Stage1 over the 4-bit paged cache; returns ``mid_o [B, Hq, S, D+1]`` (fp32).
+
+    ``S`` comes from ``mid_o`` when given, else from ``num_kv_splits``.  Empty splits
+    leave their ``mid_o`` rows untouched.
+    """
+    for t, n, dt in ((q_rot, "q_rot", torch.float32), (kv_cache, "kv_cache", torch.uint8),
+                     (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
+                     (pair_lut, "pair_lut", torch.float32)):
+        _check_tensor(t, n, dt)
+    _require(q_rot.dim() == 3, "q_rot must be [B, Hq, D]")
+    B, Hq, D = q_rot.shape
+    _require(D == HEAD_DIM, f"requires D={HEAD_DIM}")
+    _require(kv_cache.dim() == 4, "kv_cache must be [blocks, block_size, Hk, slot]")
+    _, bs, Hk, slot = kv_cache.shape
+    _require(slot == slot_bytes(D), f"requires slot_size={slot_bytes(D)}")
+    _require(Hq % Hk == 0, "Hq must be a multiple of Hk")
+    _require(block_table.dim() == 2 and block_table.size(0) == B, "block_table batch mismatch")
+    _require(seq_lens.dim() == 1 and seq_lens.size(0) == B, "seq_lens batch mismatch")
+    _require(tuple(pair_lut.shape) == (256, 2), "pair_lut must be [256, 2]")
+    if mid_o is None:
+        _require(num_kv_splits is not None and num_kv_splits > 0,
+                 "num_kv_splits is required when mid_o is None")
+        mid_o = torch.empty(B, Hq, num_kv_splits, D + 1, dtype=torch.float32, device=q_rot.device)
+    _check_tensor(mid_o, "mid_o", torch.float32)
+    S = mid_o.size(2)
+    _require(mid_o.dim() == 4 and tuple(mid_o.shape) == (B, Hq, S, D + 1),
+             f"mid_o must be [B,{Hq},S,{D + 1}]")
+    _require(num_kv_splits is None or num_kv_splits == S, "mid_o split count mismatch")
+    devs = {t.device for t in (q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o)}
+    _require(len(devs) == 1, "all tensors must be on the same device")
+    scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
+    _require(kernel in KERNELS, f"kernel must be one of {sorted(KERNELS)}")
+    rc = _lib.load().tq4_stage1_ex(
+        q_rot.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
+        pair_lut.data_ptr(), mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1),
+        kv_cache.stride(0), S, _layout_id(layout), scale, KERNELS[kernel], _stream(q_rot.device))
+    _lib.check(rc, "tq4_stage1")
+    return mid_o
+
+
+def stage2(mid_o, seq_lens, out=None, lse=None, out_dtype=torch.float32):
+    """Merge the non-empty splits; returns ``(out [B, Hq, D], lse [B, Hq])``."""
+    _check_tensor(mid_o, "mid_o", torch.float32)
+    _check_tensor(seq_lens, "seq_lens", torch.int32)
+    _require(mid_o.dim() == 4 and mid_o.size(3) == HEAD_DIM + 1, "invalid mid_o shape")
+    B, Hq, S, _ = mid_o.shape
+    if out is None:
+        out = torch.empty(B, Hq, HEAD_DIM, dtype=out_dtype, device=mid_o.device)
+    if lse is None:
+        lse = torch.empty(B, Hq, dtype=torch.float32, device=mid_o.device)
+    _require(out.is_cuda and out.is_contiguous() and out.dtype in DTYPES, "invalid output")
+    _require(tuple(out.shape) == (B, Hq, HEAD_DIM), "invalid output shape")
+    _check_tensor(lse, "lse", torch.float32)
+    _require(tuple(lse.shape) == (B, Hq), "invalid lse shape")
+    _require(seq_lens.numel() == B, "seq_lens batch mismatch")
+    rc = _lib.load().tq4_stage2(mid_o.data_ptr(), seq_lens.data_ptr(), out.data_ptr(),
+                                DTYPES[out.dtype], lse.data_ptr(), B, Hq, HEAD_DIM, S,
+                                _stream(mid_o.device))
+    _lib.check(rc, "tq4_stage2")
+    return out, lse
+
+
+def rotate_query(query, rotation_t, q_rot=None):
+    """``q_rot = query.float() @ rotation_t`` on the GPU (``reference/soa_decode_v1.py:532-538``)."""
+    _require(query.is_cuda and query.is_contiguous() and query.dtype in DTYPES, "invalid query")
+    _check_tensor(rotation_t, "rotation_t", torch.float32)
+    _require(query.size(-1) == HEAD_DIM and tuple(rotation_t.shape) == (HEAD_DIM, HEAD_DIM),
+             f"requires D={HEAD_DIM}")
+    if q_rot is None:
+        q_rot = torch.empty(query.shape, dtype=torch.float32, device=query.device)
+    _check_tensor(q_rot, "q_rot", torch.float32)
+    rows = query.numel() // HEAD_DIM
+    rc = _lib.load().tq4_rotate_query(query.data_ptr(), DTYPES[query.dtype], rotation_t.data_ptr(),
+                                      q_rot.data_ptr(), rows, HEAD_DIM, _stream(query.device))
+    _lib.check(rc, "tq4_rotate_query")
+    return q_rot
+
+
+class DecodeWorkspace:
+    """Preallocated buffers of one full decode step (fixed shapes, reusable)."""
+
+    def __init__(self, batch, num_q_heads, num_kv_splits, device, out_dtype=torch.bfloat16):
+        self.q_rot = torch.empty(batch, num_q_heads, HEAD_DIM, dtype=torch.float32, device=device)
+        self.pair_lut = torch.empty(256, 2, dtype=torch.float32, device=device)
+        self.mid_o = torch.empty(batch, num_q_heads, num_kv_splits, HEAD_DIM + 1,
+                                 dtype=torch.float32, device=device)
+        self.out = torch.empty(batch, num_q_heads, HEAD_DIM, dtype=out_dtype, device=device)
+        self.lse = torch.empty(batch, num_q_heads, dtype=torch.float32, device=device)
+
+
+def full_decode(query, rotation_t, kv_cache, block_table, seq_lens, centroids, num_kv_splits, *,
+                layout="soa", out_dtype=None, attn_scale=None, workspace=None):
+    """Rotation + pair LUT + Stage1 + Stage2 in four launches; returns ``(out, lse)``.
+
+    ``out`` is in ``out_dtype`` (default: the query dtype, as ``reference/soa_decode_v1.py:643``).
+    """
+    _require(query.is_cuda and query.is_contiguous() and query.dtype in DTYPES, "invalid query")
+    _check_tensor(rotation_t, "rotation_t", torch.float32)
+    _check_tensor(centroids, "centroids", torch.float32)
+    _require(centroids.numel() == 16, "4-bit path requires 16 centroids")
+    for t, n, dt in ((kv_cache, "kv_cache", torch.uint8), (block_table, "block_table", torch.int32),
+                     (seq_lens, "seq_lens", torch.int32)):
+        _check_tensor(t, n, dt)
+    B, Hq, D = query.shape
+    _require(D == HEAD_DIM, f"requires D={HEAD_DIM}")
+    _, bs, Hk, slot = kv_cache.shape
+    _require(slot == slot_bytes(D), f"requires slot_size={slot_bytes(D)}")
+    out_dtype = query.dtype if out_dtype is None else out_dtype
+    ws = workspace or DecodeWorkspace(B, Hq, num_kv_splits, query.device, out_dtype)
+    _require(ws.out.dtype == out_dtype and ws.mid_o.shape[:3] == (B, Hq, num_kv_splits),
+             "workspace does not match this call")
+    scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
+    rc = _lib.load().tq4_full_decode(
+        query.data_ptr(), DTYPES[query.dtype], rotation_t.data_ptr(), centroids.data_ptr(),
+        kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), ws.q_rot.data_ptr(),
+        ws.pair_lut.data_ptr(), ws.mid_o.data_ptr(), ws.out.data_ptr(), DTYPES[out_dtype],
+        ws.lse.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), kv_cache.stride(0),
+        num_kv_splits, _layout_id(layout), scale, _stream(query.device))
+    _lib.check(rc, "tq4_full_decode")
+    return ws.out, ws.lse
+
+
+# ---- reference harness call shapes -------------------------------------------------
+
+def launch_tq4_v2_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, pair_lut, mid_o=None,
+                         num_kv_splits=32):
+    """SoA Stage1 with the ``baseline/triton_v2.py:569-577`` signature."""
+    _check_tensor(centroids, "centroids", torch.float32)
+    _require(centroids.numel() == 16, "4-bit path requires 16 centroids")
+    return stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o,
+                  num_kv_splits=None if mid_o is not None else num_kv_splits, layout="soa")
+
+
+def launch_soa_v1_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o):
+    """SoA Stage1 with the ``baseline/triton_v1.py:145-152`` signature."""
+    return stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut_device(centroids), mid_o,
+                  layout="soa")
+
+
+def launch_aos_v1_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o):
+    """AoS Stage1 with the ``baseline/triton_v1.py:90-97`` signature."""
+    return stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut_device(centroids), mid_o,
+                  layout="aos")
+
+
+def launch_stage2(mid_o, seq_lens, output, lse):
+    """Stage2 with the ``baseline/stage2.py:58-63`` signature (writes in place)."""
+    stage2(mid_o, seq_lens, output, lse)
+
+
+class _CudaExtCompat:
+    """Methods named like the reference CUDA extension modules (``cuda/tq4_cuda_v*_bind.cpp``).
+
+    ``tq4_cuda_vN(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o)`` runs the SoA
+    Stage1 with the split count taken from ``mid_o``; ``tq4_cuda_v7_stage2(mid_o, output,
+    lse)`` takes ``seq_lens`` from the last Stage1 call's argument when not given, as the
+    reference kernel has no ``seq_lens`` argument; ``tq4_cuda_v7_full`` runs both.
+    """
+
+    def __init__(self):
+        self._last_seq_lens = None
+
+    def _stage1(self, q_rot, kv_cache, block_table, seq_lens, centroids, mid_o):
+        self._last_seq_lens = seq_lens
+        return launch_soa_v1_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o)
+
+    def __getattr__(self, name):
+        if name.startswith("tq4_cuda_v") and name[len("tq4_cuda_v"):].isdigit():
+            return self._stage1
+        raise AttributeError(name)
+
+    def tq4_cuda_v7_stage1(self, *args):
+        return self._stage1(*args)
+
+    def tq4_cuda_v7_stage2(self, mid_o, output, lse, seq_lens=None):
+        sl = seq_lens if seq_lens is not None else self._last_seq_lens
+        if sl is None:
+            sl = torch.full((mid_o.size(0),), mid_o.size(2), dtype=torch.int32, device=mid_o.device)
+        stage2(mid_o, sl, output, lse)
+        return output
+
+    def tq4_cuda_v7_full(self, q_rot, kv_cache, block_table, seq_lens, centroids, mid_o, output,
+                         lse):
+        self._stage1(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o)
+        stage2(mid_o, seq_lens, output, lse)
+        return output
+
+
+ext = _CudaExtCompat()
