@@ -1,0 +1,205 @@
+"""Stage1 benchmark of the MI355X TurboQuant 4-bit decode path.
+
+One step = one Stage1 launch over the whole batch of the Qwen3-4B-shaped decode
+workload (B=64, ctx 4096, 32/8 heads, D=128, KV block 16, 32 splits, SoA cache,
+random-permuted block table), inputs resident in HBM.  Each timed launch follows a
+1 GiB read sweep so the ~316 MB working set is not served from the 256 MB
+Infinity Cache (cold cache), and is bracketed by HIP events on the launch stream.
+
+Prints ONE JSON line.  ``value`` is achieved HBM GB/s = algorithmic bytes per launch /
+mean launch time; ``roofline`` relates it to MI355X's 8 TB/s; ``cpu_baseline`` is the
+C oracle (a port of the reference Stage1 math) timed on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout soa|aos]
+                       [--kernel auto|mfma|simple] [--no-cpu-baseline] [--calibrate-copy]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import re
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "turboquant-cuda-decode_amd"))
+
+METRIC = ("Stage1 µs + achieved HBM GB/s (% of peak), B64×ctx4096 Qwen3-4B shape, 1 GPU")
+HBM_PEAK_GBS = 8000.0
+FLUSH_BYTES = 1 << 30
+PROFILES = ROOT / "profiles"
+
+
+def algorithmic_bytes(w) -> int:
+    """Bytes a Stage1 launch must move: every live token's 134-byte K/V slot per kv-head,
+    q_rot, the used block-table entries, seq_lens, the pair LUT, and the mid_o rows of
+    the non-empty splits (D+1 floats per q-head)."""
+    import numpy as np
+
+    seq = w.seq_lens.astype(np.int64)
+    bs, S = w.block_size, w.num_kv_splits
+    kv = int(seq.sum()) * w.num_kv_heads * 134
+    q = w.q_rot.nbytes
+    bt = int(((seq + bs - 1) // bs).sum()) * 4
+    split_len = (seq + S - 1) // S
+    live = np.minimum(S, (seq + split_len - 1) // np.maximum(split_len, 1))
+    mid = int(live.sum()) * w.num_q_heads * (w.head_dim + 1) * 4
+    return kv + q + bt + w.seq_lens.nbytes + 256 * 2 * 4 + mid
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, if one exists."""
+    path = PROFILES / f"{name}_pmc.md"
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w, threads: int, repeats: int = 3):
+    from oracle import native
+
+    native.lib()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        native.stage1(w.q_rot, w.kv_cache, w.block_table, w.seq_lens, w.centroids,
+                      w.num_kv_splits, num_kv_heads=w.num_kv_heads, threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(algorithmic_bytes(w) / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "seconds": round(t, 4),
+            "sample": (f"whole workload ({w.batch} seqs x {int(w.seq_lens[0])} tokens, SoA), "
+                       f"C oracle tq4o_stage1 (Triton V1 program restated, fp32, OpenMP), "
+                       f"median of {repeats}")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layout", default="soa", choices=["soa", "aos"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "mfma", "simple"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-variants", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 256 MiB device copy (PMC byte-counter calibration)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this path has no multi-GPU form "
+              f"(--gpus {args.gpus}, WORLD_SIZE {world}); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from tq4_decode import ops, workloads
+
+    dev = torch.device("cuda:0")
+    w = workloads.qwen3_4b_b64_ctx4096()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    q, bt, sl, lut = t(w.q_rot), t(w.block_table), t(w.seq_lens), t(w.pair_lut)
+    caches = {"soa": t(w.kv_cache)}
+    if args.layout == "aos" or not args.no_variants:
+        caches["aos"] = t(workloads.soa_to_aos(w.kv_cache, w.centroids, w.num_kv_heads))
+    mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
+    flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
+    nbytes = algorithmic_bytes(w)
+
+    def launch(layout, kernel):
+        ops.stage1(q, caches[layout], bt, sl, lut, mid, layout=layout, kernel=kernel)
+
+    def cold_times(layout, kernel, steps, warmup):
+        for _ in range(warmup):
+            flush.sum()
+            launch(layout, kernel)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        for a, b in ev:
+            flush.sum()  # 1 GiB read sweep: evicts L2 and the Infinity Cache
+            a.record()
+            launch(layout, kernel)
+            b.record()
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) for a, b in ev]
+
+    def warm_time(layout, kernel, iters=100, rounds=5):
+        res = []
+        for _ in range(rounds):
+            for _ in range(10):
+                launch(layout, kernel)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(iters):
+                launch(layout, kernel)
+            b.record()
+            torch.cuda.synchronize()
+            res.append(a.elapsed_time(b) / iters)
+        return statistics.median(res)
+
+    torch.cuda.synchronize()
+    ms = cold_times(args.layout, args.kernel, args.steps, args.warmup)
+    mean_ms = statistics.fmean(ms)
+    med_ms = statistics.median(ms)
+    gbs = nbytes / (mean_ms * 1e-3) / 1e9
+    kname = f"stage1_{'mfma' if args.kernel in ('auto', 'mfma') else 'simple'}_{args.layout}_qwen3_4b_b64_ctx4096"
+    traffic = traffic_from_profile(kname)
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded CPU generator: uniform random 4-bit code bytes, fp16 "
+                "norm/scale/zero, random-permuted block table)",
+        "config": {"workload": "qwen3_4b_b64_ctx4096", "batch": w.batch, "ctx": 4096,
+                   "q_heads": w.num_q_heads, "kv_heads": w.num_kv_heads, "head_dim": w.head_dim,
+                   "block_size": w.block_size, "num_kv_splits": w.num_kv_splits,
+                   "layout": args.layout, "kernel": args.kernel, "cache": "cold (1 GiB sweep)"},
+        "stage1_us": round(mean_ms * 1e3, 2),
+        "stage1_us_median": round(med_ms * 1e3, 2),
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "algorithmic_bytes": nbytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
+    }
+    if not args.no_variants:
+        var = {}
+        for layout, kernel in (("soa", "mfma"), ("aos", "mfma"), ("soa", "simple")):
+            vm = statistics.fmean(cold_times(layout, kernel, 50, 5))
+            var[f"{layout}_{kernel}_cold_us"] = round(vm * 1e3, 2)
+            var[f"{layout}_{kernel}_warm_us"] = round(warm_time(layout, kernel) * 1e3, 2)
+        result["variants"] = var
+    if args.calibrate_copy:
+        src = torch.empty(1 << 26, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            flush.sum()
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = src.nbytes
+    if not args.no_cpu_baseline:
+        try:
+            threads = min(16, len(os.sched_getaffinity(0)))
+        except AttributeError:
+            threads = min(16, os.cpu_count() or 1)
+        result["cpu_baseline"] = cpu_baseline(w, threads)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

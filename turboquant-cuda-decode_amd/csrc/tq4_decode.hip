@@ -41,6 +41,13 @@ int launch_status(const char *what) {
 
 bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+int log2_int(int x) {
+    int r = 0;
+    while ((1 << r) < x)
+        ++r;
+    return r;
+}
+
 struct Stage1Args {
     const float *q_rot;
     const uint8_t *cache;
@@ -87,8 +94,8 @@ template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t
 template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_t st) {
     const dim3 grid(a.S, a.Hk, a.B);
     hipLaunchKernelGGL((tq4::stage1_mfma_kernel<LAYOUT, NSET>), grid, dim3(tq4::kWave), 0, st,
-                       a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk, a.bs,
-                       a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
+                       a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk,
+                       log2_int(a.bs), a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
 
 template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
@@ -107,13 +114,14 @@ template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
 
 bool mfma_applies(const Stage1Args &a) {
     const int g = a.Hq / a.Hk;
-    return (g == 4 || g == 8) && a.bs % 16 == 0 && a.stride % 16 == 0;
+    const bool pow2 = a.bs >= 16 && (a.bs & (a.bs - 1)) == 0;
+    return (g == 4 || g == 8) && pow2 && a.stride % 16 == 0;
 }
 
 template <int LAYOUT> int dispatch_mfma(const Stage1Args &a, hipStream_t st) {
     if (!mfma_applies(a))
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: MFMA kernel needs GQA group 4 or 8, "
-                                       "block_size %% 16 == 0 and a 16-byte block stride");
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: MFMA kernel needs GQA group 4 or 8, a "
+                                       "power-of-two block_size >= 16 and a 16-byte block stride");
     if (a.Hq / a.Hk == 4)
         launch_mfma<LAYOUT, 1>(a, st);
     else

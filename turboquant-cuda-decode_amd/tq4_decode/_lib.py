@@ -7,11 +7,14 @@ loaded, and torch's stream handles are valid in library calls.
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 
 import torch  # noqa: F401  (see module docstring)
 
-LIB_PATH = pathlib.Path(__file__).resolve().parent / "libtq4_decode.so"
+# TQ4_DECODE_LIB selects another build of the same library (e.g. for A/B timing).
+LIB_PATH = pathlib.Path(os.environ.get("TQ4_DECODE_LIB") or
+                        pathlib.Path(__file__).resolve().parent / "libtq4_decode.so")
 
 EXPORTS = (
     "tq4_stage1",

@@ -25,6 +25,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     # keep hipcc from emitting packed-fp32 VALU ops
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: no AGPR<->VGPR copies around the softmax rescale
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
 ]
 
