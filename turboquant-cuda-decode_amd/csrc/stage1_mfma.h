@@ -2,41 +2,45 @@
 // GQA group G = 4 * NSET, 16-token tiles aligned to the KV block.
 //
 // Lane l = 16u + 4v + c (u, v, c in 0..3).  MFMA block = l / 4 = 4u + v, in-block
-// index = c.  The 4x4 MFMA shapes put 4 tokens (or 4 dims) on the rows and the 4
-// heads of a head set on the columns, so the GQA group costs no padding.
+// index = c.  All products run on v_mfma_f32_4x4x1f32 (fp32 operands, 16 blocks); its
+// 4x4 shape puts 4 tokens or 4 dims against the 4 heads of a head set, so the GQA
+// group costs no padding.  On gfx950 vector instructions do not overlap fp32 MFMAs,
+// so the layout is chosen to keep the vector work per tile small.
 //
-// QK^T of a tile (tokens 4u + i, i = 0..3) on v_mfma_f32_4x4x1f32 (fp32 operands):
-//   A[block][row i] = K[4u + i][32v + s]      lane (u,v,c) decodes token 4u + c,
-//   B[block][col j] = q[head j][32v + s]      dims 32v .. 32v+31 (16 code bytes,
-//   32 steps s; result lane (u,v,j) reg i     one 16-byte load).
-//   B needs the same value in the four lane groups u, so it is broadcast from lane
-//   group s % 4 by the MFMA's B lane-group pattern (blgp = 4 + s % 4): lane (g,v,c)
-//   holds q[c][32v + 4k + g] in register k, 8 registers per head set.
-//   = partial dot over dim group v.  The centroids come from a 256-entry LDS table
-//   indexed by the packed code byte (entry = (c[low nibble], c[high nibble])): one
-//   ds_read_b64 per byte gives the A operands of two MFMAs.  q is pre-scaled by
-//   attn_scale * log2(e).  Two DPP row rotations (ror 8, ror 4) sum the four dim
-//   groups, leaving the score of token 4u + i, head c in every lane (u,*,c).
-// Softmax: each lane keeps the running (m, l, z) of its slot u and head c.  All four
-//   lanes (u, 0..3, c) hold identical scores, so their states agree.  The running max
-//   only moves when a score exceeds it by more than kRescaleLog2 (p <= 2^8), so the
-//   32-register rescale is rare after the first tile; slots merge once at the end.
-// PV of the tile on v_mfma_f32_4x4x1f32 (fp32 operands), step i (token 4u + i), 8
-//   MFMAs k = 0..7:
-//   A[block][row r] = code[4u + i][32v + 8r + k]   lane (u,v,c) loads one V dword
-//   B[block][col j] = p[head j][4u + i] * scale    (its own softmax weight)
-//   result lane (u,v,j) reg r += O[head j][32v + 8r + k]   (32 accumulators / set)
-//   The V zero term sum_t p_t * zero_t is kept per lane and added at the end.
+// QK^T of a tile (tokens 4u .. 4u+3 in lane group u):
+//   lane (u,v,c) loads the 16 K code bytes of token 4u + ((c + v) & 3), dims 32v ..
+//   32v+31.  A[block (u,v)][row i] = K[4u + ((i + v) & 3)][32v + s] (lane (u,v,i)),
+//   B[block][col j] = q[head j][32v + s], broadcast from lane group s % 4 by the
+//   B lane-group pattern (blgp = 4 + s % 4): lane (g,v,c) holds q[c][32v + 4k + g] in
+//   register k.  32 MFMAs (one per dim of the group) leave in lane (u,v,c) register i
+//   the dot over dim group v of token 4u + ((i + v) & 3) with head c.  The centroids
+//   come from a 256-entry LDS table indexed by the packed code byte (entry = (c[low
+//   nibble], c[high nibble])): one ds_read_b64 gives the A operands of two MFMAs.
+//   Because of the rotation, register k of lane (u, v-k, c) holds token 4u+v's dot
+//   over group v-k, so three DPP row rotations (by 4, 8, 12 lanes) sum the full score
+//   of token 4u + v, head c into lane (u,v,c): one score per lane, no duplicates.
+// Softmax: lane (u,v,c) owns token 4u+v, head c.  Slot (u, c) (four lanes v) keeps a
+//   running max m; the max only moves when a score exceeds it by more than
+//   kRescaleLog2 (p <= 2^8), so the rescale branch is rare after a slot's first tile.
+//   Each lane accumulates its own l and z (z = sum p * V zero); slots merge at the end.
+// PV of the tile, step i (token 4u + i), 8 MFMAs k = 0..7:
+//   A[block (u,v)][row h] = p[head h][4u + i] * V scale   -- the A operand of block
+//     (u, i), broadcast to the four blocks of lane group u (cbsz = 2, abid = i), i.e.
+//     exactly where the softmax left it;
+//   B[block (u,v)][col j] = code[4u + i][32v + 8j + k]    -- lane (u,v,j) loads the V
+//     dword of token 4u+i at dims 32v + 8j .. +7;
+//   result lane (u,v,j) reg h += O[head h][32v + 8j + k] (32 accumulators per set).
+//   V codes are converted two at a time with v_cvt_pk_f32_fp8: a byte n < 16 read as
+//   fp8 (e4m3) is exactly n * 2^-9; the power-of-two factor is undone at the end.
 //
 // Schedule: stage j = softmax of tile j, then PV of tile j together with QK^T of tile
-// j+1 in one branch-free block (software pipelining across tiles), so matrix-core and
-// vector work from two tiles overlap within a wave.
+// j+1 in one branch-free block (software pipelining across tiles).
 //
 // Memory: the block-table entries of up to 64 tiles are read once (one lane per tile)
 // and broadcast with readlane.  A 4-slot register ring keeps the loads of the next
-// tiles in flight (~6.6-8.8 KB per wave).  Loads are buffer loads off a per-tile
-// descriptor whose base is the KV block (offsets are per-lane constants), plain and
-// unconditional, so the compiler's wait before each tile is exact.
+// tiles in flight.  Loads are buffer loads off a per-tile descriptor whose base is the
+// KV block (offsets are per-lane constants), plain and unconditional, so the
+// compiler's wait before each tile is exact.
 #pragma once
 #include "tq4_device.h"
 
@@ -44,35 +48,34 @@ namespace tq4 {
 
 constexpr float kRescaleLog2 = 8.0f;
 
-
 template <int CTRL> __device__ __forceinline__ float dpp(float x) {
     return __builtin_bit_cast(
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
-// Sum over the four lanes of a 16-lane row that share (lane & 3).
+// DPP row_ror:N -- lane r of a 16-lane row reads lane (r - N) mod 16.
+constexpr int kRor4 = 0x124, kRor8 = 0x128, kRor12 = 0x12C;
+// Sum / max over the four lanes of a 16-lane row that share (lane & 3).
 __device__ __forceinline__ float row_group_sum(float x) {
-    x += dpp<0x128>(x);  // row_ror:8
-    x += dpp<0x124>(x);  // row_ror:4
+    x += dpp<kRor8>(x);
+    x += dpp<kRor4>(x);
     return x;
+}
+__device__ __forceinline__ float row_group_max(float x) {
+    x = fmaxf(x, dpp<kRor8>(x));
+    return fmaxf(x, dpp<kRor4>(x));
 }
 // Value of quad lane Q broadcast to the whole quad.
 template <int Q> __device__ __forceinline__ float quad_bcast(float x) {
     return dpp<(Q | (Q << 2) | (Q << 4) | (Q << 6))>(x);
 }
 
-__device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
-}
-// Same, with B taken from lane group G (lanes 16G .. 16G+15) for all four groups.
+// B taken from lane group G (lanes 16G .. 16G+15) for all four groups.
 template <int G> __device__ __forceinline__ floatx4 mfma_f32_bcast(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 4 + G);
 }
-
-// Hide a value's provenance from the optimiser so byte-wise decodes stay single
-// instructions (v_cvt_f32_ubyteN) instead of being re-derived with extra shifts.
-__device__ __forceinline__ uint32_t opaque(uint32_t x) {
-    __asm__("" : "+v"(x));
-    return x;
+// A taken from block I of each lane group (cbsz = 2, abid = I).
+template <int I> __device__ __forceinline__ floatx4 mfma_f32_abcast(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 2, I, 0);
 }
 
 // K-code table entry for one packed byte (low nibble = even dim, high nibble = odd
@@ -95,36 +98,33 @@ __device__ __forceinline__ void build_key_table(typename KEntry<LAYOUT>::type *t
     }
 }
 
-// Registers one tile needs (decoded view).
-struct TileRegs {
-    uint4 k;       // own token's 16 K code bytes (dims 32v .. 32v+31)
-    uint32_t v[4]; // V code dword of token 4u + i (dims 32v + 8c .. +7)
-    uint2 m[3];    // SoA: fp16 norm / scale / zero of tokens 4u .. 4u+3
-                   // AoS: m[0].x = own norm, m[0].y = own scale, m[1].x = own zero
-};
-
 // Per-lane byte offsets inside one KV block (fixed for a kernel instance).
 struct LaneOffsets {
-    uint32_t k, v[4], m, mf;  // mf: SoA distance between the three metadata arrays
+    uint32_t k;     // K bytes of token 4u + ((c+v) & 3), dims 32v ..
+    uint32_t v[4];  // V dword of token 4u + i, dims 32v + 8c ..
+    uint32_t m;     // SoA: norm of token 4u + v; AoS: slot of token 4u + v
+    uint32_t mf;    // SoA: distance between the three metadata arrays
 };
 
 template <int LAYOUT>
 __device__ __forceinline__ LaneOffsets lane_offsets(int u, int v, int c, int kvh, int hk,
                                                     int block_size) {
     LaneOffsets o;
+    const int kt = 4 * u + ((c + v) & 3);
+    const int st = 4 * u + v;
     if (LAYOUT == 0) {
-        o.k = ((4 * u + c) * hk + kvh) * kSoaRecord + 16 * v;
+        o.k = (kt * hk + kvh) * kSoaRecord + 16 * v;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             o.v[i] = ((4 * u + i) * hk + kvh) * kSoaRecord + kHalfD + 16 * v + 4 * c;
-        o.m = block_size * hk * kSoaRecord + (kvh * 3 * block_size + 4 * u) * 2;
+        o.m = block_size * hk * kSoaRecord + (kvh * 3 * block_size + st) * 2;
         o.mf = block_size * 2;
     } else {
-        o.k = ((4 * u + c) * hk + kvh) * kAosSlot + 16 * v;  // 2-byte aligned
+        o.k = (kt * hk + kvh) * kAosSlot + 16 * v;  // 2-byte aligned
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             o.v[i] = ((4 * u + i) * hk + kvh) * kAosSlot + kHalfD + 2 + 16 * v + 4 * c;
-        o.m = ((4 * u + c) * hk + kvh) * kAosSlot;  // own slot start
+        o.m = (st * hk + kvh) * kAosSlot;
         o.mf = 0;
     }
     return o;
@@ -135,17 +135,23 @@ template <int LAYOUT> struct RawTile;
 template <> struct RawTile<0> {
     uint4 k;
     uint32_t v[4];
-    uint2 m[3];
+    uint32_t norm, scale, zero;  // fp16 bits of token 4u + v
 };
 template <> struct RawTile<1> {
-    uint32_t k[5];  // aligned dwords around the own (2-byte aligned) K bytes
+    uint32_t k[5];  // aligned dwords around the (2-byte aligned) K bytes
     uint2 v[4];     // aligned dword pairs around each V dword
-    unsigned short norm, scale, zero;
+    uint32_t norm, scale, zero;
+};
+
+// Decoded view of a tile.
+struct TileRegs {
+    uint4 k;
+    uint32_t v[4];
+    uint32_t norm, scale, zero;
 };
 
 // Loads of one tile.  rsrc: buffer descriptor based at the KV block; doff / moff: byte
 // offsets of the tile's 16-token piece inside the block (data records / SoA metadata).
-// Offsets are the per-lane constants of lane_offsets().
 template <int LAYOUT>
 __device__ __forceinline__ void issue_tile(RawTile<LAYOUT> &t, __amdgpu_buffer_rsrc_t rsrc,
                                            int doff, int moff, const LaneOffsets &o) {
@@ -154,10 +160,9 @@ __device__ __forceinline__ void issue_tile(RawTile<LAYOUT> &t, __amdgpu_buffer_r
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v[i], doff, 0);
-#pragma unroll
-        for (int f = 0; f < 3; ++f)
-            t.m[f] = __builtin_bit_cast(
-                uint2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, o.m + f * o.mf, moff, 0));
+        t.norm = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff, 0);
+        t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + o.mf, moff, 0);
+        t.zero = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + 2 * o.mf, moff, 0);
     } else {
         const uint32_t ka = o.k & ~3u;
         const auto k03 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ka, doff, 0);
@@ -176,7 +181,6 @@ __device__ __forceinline__ void issue_tile(RawTile<LAYOUT> &t, __amdgpu_buffer_r
     }
 }
 
-// Decoded view of a tile's registers (AoS dwords funnel-shifted into place).
 template <int LAYOUT>
 __device__ __forceinline__ TileRegs decode_tile(const RawTile<LAYOUT> &t, const LaneOffsets &o) {
     TileRegs r;
@@ -185,9 +189,6 @@ __device__ __forceinline__ TileRegs decode_tile(const RawTile<LAYOUT> &t, const 
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             r.v[i] = t.v[i];
-#pragma unroll
-        for (int f = 0; f < 3; ++f)
-            r.m[f] = t.m[f];
     } else {
         const uint32_t sh = o.k & 3u;
         r.k.x = __builtin_amdgcn_alignbyte(t.k[1], t.k[0], sh);
@@ -197,15 +198,20 @@ __device__ __forceinline__ TileRegs decode_tile(const RawTile<LAYOUT> &t, const 
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             r.v[i] = __builtin_amdgcn_alignbyte(t.v[i].y, t.v[i].x, o.v[i] & 3u);
-        r.m[0] = uint2{t.norm, t.scale};
-        r.m[1] = uint2{t.zero, 0u};
-        r.m[2] = uint2{0u, 0u};
     }
+    r.norm = t.norm;
+    r.scale = t.scale;
+    r.zero = t.zero;
     return r;
 }
 
+__device__ __forceinline__ float half_lo(uint32_t w) { return half_bits_to_float(w); }
+
+// Running softmax state of lane (u,v,c): slot (u, head c) shares m across v; l and z are
+// the lane's own partial sums; acc[set][k] reg h = O[head h][32v + 8c + k] of slot u.
 template <int NSET> struct SoftmaxState {
-    float m[NSET], l[NSET], z[NSET];
+    float negm[NSET];  // -m (exp2 domain); starts at +FLT_MAX: "no token seen yet"
+    float l[NSET], z[NSET];
     floatx4 acc[NSET][8];
 };
 
@@ -214,13 +220,10 @@ template <int NSET> struct QOperands {
     float v[NSET][8];
 };
 
-__device__ __forceinline__ float half_lo(uint32_t w) { return half_bits_to_float(w); }
-__device__ __forceinline__ float half_hi(uint32_t w) { return half_bits_to_float(w >> 16); }
-
-// Partial QK^T dots of one tile (two accumulation chains per head set) and, for AoS,
-// the lane's share of ||c[idx]||^2 of its own token.
+// Dots of one tile (one MFMA chain per head set) and, for AoS, the lane's share of
+// ||c[idx]||^2 of its K token.
 template <int NSET> struct TileScores {
-    floatx4 sc0[NSET], sc1[NSET];
+    floatx4 sc[NSET];
     float csq_part;
 };
 
@@ -228,10 +231,8 @@ template <int LAYOUT, int NSET>
 __device__ __forceinline__ void qk_tile(const uint4 &k, const typename KEntry<LAYOUT>::type *ktab,
                                         const QOperands<NSET> &q, TileScores<NSET> &s) {
 #pragma unroll
-    for (int set = 0; set < NSET; ++set) {
-        s.sc0[set] = floatx4{0.f, 0.f, 0.f, 0.f};
-        s.sc1[set] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int set = 0; set < NSET; ++set)
+        s.sc[set] = floatx4{0.f, 0.f, 0.f, 0.f};
     s.csq_part = 0.f;
     const uint32_t kwords[4] = {k.x, k.y, k.z, k.w};
 #pragma unroll
@@ -243,116 +244,108 @@ __device__ __forceinline__ void qk_tile(const uint4 &k, const typename KEntry<LA
         for (int set = 0; set < NSET; ++set) {
             // dims 2b and 2b+1 = 4k + g with k = b / 2, g = 2 (b % 2) + {0, 1}
             if (bidx & 1) {
-                s.sc0[set] = mfma_f32_bcast<2>(e.x, q.v[set][bidx >> 1], s.sc0[set]);
-                s.sc1[set] = mfma_f32_bcast<3>(e.y, q.v[set][bidx >> 1], s.sc1[set]);
+                s.sc[set] = mfma_f32_bcast<2>(e.x, q.v[set][bidx >> 1], s.sc[set]);
+                s.sc[set] = mfma_f32_bcast<3>(e.y, q.v[set][bidx >> 1], s.sc[set]);
             } else {
-                s.sc0[set] = mfma_f32_bcast<0>(e.x, q.v[set][bidx >> 1], s.sc0[set]);
-                s.sc1[set] = mfma_f32_bcast<1>(e.y, q.v[set][bidx >> 1], s.sc1[set]);
+                s.sc[set] = mfma_f32_bcast<0>(e.x, q.v[set][bidx >> 1], s.sc[set]);
+                s.sc[set] = mfma_f32_bcast<1>(e.y, q.v[set][bidx >> 1], s.sc[set]);
             }
         }
     }
 }
 
-// Scores of one tile -> per-slot online softmax update -> PV weights pw (p * V scale).
-// MASKED selects the path for a tile that straddles the split boundary (tokens outside
-// [start, end) get p = 0).
-template <int LAYOUT, int NSET, bool MASKED>
+// Full score of token 4u+v (head c) from the rotated partial dots.
+__device__ __forceinline__ float gather_score(const floatx4 &sc) {
+    float s = sc[0] + dpp<kRor4>(sc[1]);
+    s += dpp<kRor8>(sc[2]);
+    return s + dpp<kRor12>(sc[3]);
+}
+
+// ||c[idx]||^2 of token 4u+v from the per-lane shares (lane (v', c') holds the share of
+// token 4u + ((c' + v') & 3) over dim group v').
+__device__ __forceinline__ float gather_csq(float x) {
+    float s = quad_bcast<0>(x);
+    s += dpp<kRor4>(quad_bcast<1>(x));
+    s += dpp<kRor8>(quad_bcast<2>(x));
+    return s + dpp<kRor12>(quad_bcast<3>(x));
+}
+
+// Softmax of one tile -> PV weights pw (p * V scale).  `valid` is false for tokens outside
+// the split (only boundary tiles have any).
+template <int LAYOUT, int NSET>
 __device__ __forceinline__ void softmax_tile(const TileScores<NSET> &s, const TileRegs &t,
-                                             SoftmaxState<NSET> &st, float (&pw)[NSET][4],
-                                             int tok0, int start, int end) {
-    // per-token factors: K norm (score is already in the exp2 domain), V scale/zero
-    float norm[4], vscale[4], vzero[4];
+                                             SoftmaxState<NSET> &st, float (&pw)[NSET],
+                                             bool boundary, bool valid) {
+    const _Float16 scale_h = __builtin_bit_cast(_Float16, (unsigned short)t.scale);
+    const _Float16 zero_h = __builtin_bit_cast(_Float16, (unsigned short)t.zero);
+    float norm;
     if constexpr (LAYOUT == 0) {
-        norm[0] = half_lo(t.m[0].x);
-        norm[1] = half_hi(t.m[0].x);
-        norm[2] = half_lo(t.m[0].y);
-        norm[3] = half_hi(t.m[0].y);
-        vscale[0] = half_lo(t.m[1].x);
-        vscale[1] = half_hi(t.m[1].x);
-        vscale[2] = half_lo(t.m[1].y);
-        vscale[3] = half_hi(t.m[1].y);
-        vzero[0] = half_lo(t.m[2].x);
-        vzero[1] = half_hi(t.m[2].x);
-        vzero[2] = half_lo(t.m[2].y);
-        vzero[3] = half_hi(t.m[2].y);
+        norm = (float)__builtin_bit_cast(_Float16, (unsigned short)t.norm);
     } else {
-        const float csq = row_group_sum(s.csq_part);  // ||c[idx]||^2 of token 4u + c
-        const float own_ks = half_lo(t.m[0].x) * (1.0f / sqrtf(csq + 1e-16f));
-        const float own_scale = half_lo(t.m[0].y);
-        const float own_zero = half_lo(t.m[1].x);
-        norm[0] = quad_bcast<0>(own_ks);
-        norm[1] = quad_bcast<1>(own_ks);
-        norm[2] = quad_bcast<2>(own_ks);
-        norm[3] = quad_bcast<3>(own_ks);
-        vscale[0] = quad_bcast<0>(own_scale);
-        vscale[1] = quad_bcast<1>(own_scale);
-        vscale[2] = quad_bcast<2>(own_scale);
-        vscale[3] = quad_bcast<3>(own_scale);
-        vzero[0] = quad_bcast<0>(own_zero);
-        vzero[1] = quad_bcast<1>(own_zero);
-        vzero[2] = quad_bcast<2>(own_zero);
-        vzero[3] = quad_bcast<3>(own_zero);
-    }
-    bool valid[4] = {true, true, true, true};
-    if (MASKED) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            valid[i] = tok0 + i >= start && tok0 + i < end;
+        const float csq = gather_csq(s.csq_part);
+        norm = half_lo(t.norm) * __builtin_amdgcn_rsqf(csq + 1e-16f);
     }
 #pragma unroll
     for (int set = 0; set < NSET; ++set) {
-        float s2[4];
+        const float dot = gather_score(s.sc[set]);
+        float s2 = fmaf(dot, norm, st.negm[set]);  // score - m
+        if (boundary)
+            s2 = valid ? s2 : -INFINITY;
+        const float tmax = row_group_max(s2);
+        const bool need = tmax > kRescaleLog2;
+        if (__builtin_expect(__any(need), 0)) {
+            // New slot max from the exact scores (s2 is inexact while -m = FLT_MAX).
+            float sn = dot * norm;
+            if (boundary)
+                sn = valid ? sn : -INFINITY;
+            const float mt = row_group_max(sn);
+            const float negm_new = need ? -mt : st.negm[set];
+            // exp2(m_old - m_new): 1 for slots that keep their max, 0 for a first token
+            const float alpha = __builtin_amdgcn_exp2f(negm_new - st.negm[set]);
+            const float a0 = quad_bcast<0>(alpha), a1 = quad_bcast<1>(alpha);
+            const float a2 = quad_bcast<2>(alpha), a3 = quad_bcast<3>(alpha);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float dot = row_group_sum(s.sc0[set][i] + s.sc1[set][i]);
-            s2[i] = dot * norm[i];
-            if (MASKED)
-                s2[i] = valid[i] ? s2[i] : -INFINITY;
-        }
-        const float tmax = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
-        const bool need = tmax > st.m[set] + kRescaleLog2;
-        if (__any(need)) {
-            const float mnew = need ? tmax : st.m[set];
-            const float alpha = need ? __builtin_amdgcn_exp2f(st.m[set] - mnew) : 1.f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                st.acc[set][k] *= alpha;
+            for (int k = 0; k < 8; ++k) {
+                st.acc[set][k][0] *= a0;
+                st.acc[set][k][1] *= a1;
+                st.acc[set][k][2] *= a2;
+                st.acc[set][k][3] *= a3;
+            }
             st.l[set] *= alpha;
             st.z[set] *= alpha;
-            st.m[set] = mnew;
+            st.negm[set] = negm_new;
+            s2 = sn + negm_new;
         }
-        const float m_eff = MASKED && st.m[set] == -INFINITY ? 0.f : st.m[set];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float p = __builtin_amdgcn_exp2f(s2[i] - m_eff);
-            st.l[set] += p;
-            if (MASKED) {
-                st.z[set] += valid[i] ? p * vzero[i] : 0.f;
-                pw[set][i] = valid[i] ? p * vscale[i] : 0.f;
-            } else {
-                st.z[set] = fmaf(p, vzero[i], st.z[set]);
-                pw[set][i] = p * vscale[i];
-            }
-        }
+        const float p = __builtin_amdgcn_exp2f(s2);
+        st.l[set] += p;
+        st.z[set] = fmaf(p, (float)zero_h, st.z[set]);
+        pw[set] = p * (float)scale_h;
     }
 }
 
-// PV of one tile on the matrix cores (fp32 operands).
+// PV of one tile on the matrix cores: token 4u+i's weights come from block (u, i).
 template <int NSET>
-__device__ __forceinline__ void pv_tile(const TileRegs &t, const float (&pw)[NSET][4],
+__device__ __forceinline__ void pv_tile(const TileRegs &t, const float (&pw)[NSET],
                                         SoftmaxState<NSET> &st) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = opaque(t.v[i] & 0x0F0F0F0Fu);
-        const uint32_t hi = opaque((t.v[i] >> 4) & 0x0F0F0F0Fu);
+        const uint32_t lo = t.v[i] & 0x0F0F0F0Fu;         // codes of dims 8c + 0, 2, 4, 6
+        const uint32_t hi = (t.v[i] >> 4) & 0x0F0F0F0Fu;  // codes of dims 8c + 1, 3, 5, 7
+        const auto c02 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+        const auto c46 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+        const auto c13 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+        const auto c57 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+        const float code[8] = {c02[0], c13[0], c02[1], c13[1], c46[0], c57[0], c46[1], c57[1]};
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-            const float c0 = (float)((lo >> (8 * qq)) & 0xFFu);
-            const float c1 = (float)((hi >> (8 * qq)) & 0xFFu);
+        for (int set = 0; set < NSET; ++set) {
 #pragma unroll
-            for (int set = 0; set < NSET; ++set) {
-                st.acc[set][2 * qq] = mfma_f32(c0, pw[set][i], st.acc[set][2 * qq]);
-                st.acc[set][2 * qq + 1] = mfma_f32(c1, pw[set][i], st.acc[set][2 * qq + 1]);
+            for (int k = 0; k < 8; ++k) {
+                switch (i) {
+                case 0: st.acc[set][k] = mfma_f32_abcast<0>(pw[set], code[k], st.acc[set][k]); break;
+                case 1: st.acc[set][k] = mfma_f32_abcast<1>(pw[set], code[k], st.acc[set][k]); break;
+                case 2: st.acc[set][k] = mfma_f32_abcast<2>(pw[set], code[k], st.acc[set][k]); break;
+                default: st.acc[set][k] = mfma_f32_abcast<3>(pw[set], code[k], st.acc[set][k]); break;
+                }
             }
         }
     }
@@ -395,7 +388,7 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
     SoftmaxState<NSET> st;
 #pragma unroll
     for (int set = 0; set < NSET; ++set) {
-        st.m[set] = -INFINITY;
+        st.negm[set] = __FLT_MAX__;
         st.l[set] = 0.f;
         st.z[set] = 0.f;
 #pragma unroll
@@ -407,6 +400,9 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
     const int tile_first = rng.start & ~15;
     const int ntiles = (((rng.end - 1) & ~15) - tile_first) / 16 + 1;
+    // lane's softmax token relative to the split start, at tile 0
+    const int rel0 = tile_first + 4 * u + v - rng.start;
+    const uint32_t span = (uint32_t)(rng.end - rng.start);
     __syncthreads();
 
     // Issue the loads of tile j (global index) into ring slot r; its block id sits in
@@ -424,19 +420,17 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
         __builtin_amdgcn_sched_barrier(0);
     };
     // Stage j: softmax of tile j (scores computed by the previous stage), then one
-    // branch-free block with PV of tile j and QK^T of tile j+1, so the two MFMA streams
-    // and the decode VALU work interleave.  QK^T of the stage after the chunk's last
-    // tile reads a clamped (valid) tile and its scores are discarded.
+    // branch-free block with PV of tile j and QK^T of tile j+1, so the MFMA streams and
+    // the decode work interleave.  QK^T after the chunk's last tile reads a clamped
+    // (valid) tile and its scores are discarded.
     TileScores<NSET> sc;
     auto stage = [&](const RawTile<LAYOUT> &cur, const RawTile<LAYOUT> &nxt, int j) {
         const TileRegs t = decode_tile<LAYOUT>(cur, off);
         const int t0 = tile_first + 16 * j;
-        const int tok0 = t0 + 4 * u;
-        float pw[NSET][4];
-        if (t0 >= rng.start && t0 + 16 <= rng.end)
-            softmax_tile<LAYOUT, NSET, false>(sc, t, st, pw, tok0, rng.start, rng.end);
-        else
-            softmax_tile<LAYOUT, NSET, true>(sc, t, st, pw, tok0, rng.start, rng.end);
+        const bool boundary = !(t0 >= rng.start && t0 + 16 <= rng.end);
+        const bool valid = (uint32_t)(rel0 + 16 * j) < span;
+        float pw[NSET];
+        softmax_tile<LAYOUT, NSET>(sc, t, st, pw, boundary, valid);
         pv_tile<NSET>(t, pw, st);
         qk_tile<LAYOUT, NSET>(decode_tile<LAYOUT>(nxt, off).k, ktab, q, sc);
     };
@@ -472,32 +466,52 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
     }
 
     // ---- merge the four slots u and write this split's rows
+    // fp8 decode factor: a V code n was accumulated as n * code_unit
+    const float inv_code_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
 #pragma unroll
     for (int set = 0; set < NSET; ++set) {
-        float mx = fmaxf(st.m[set], __shfl_xor(st.m[set], 16, kWave));
+        // slot (u, head c): max, and l / z summed over the slot's four lanes v
+        const float m = -st.negm[set];
+        float mx = fmaxf(m, __shfl_xor(m, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float f = st.m[set] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[set] - mx);
-        float lt = f * st.l[set];
+        const float f = __builtin_amdgcn_exp2f(m - mx);  // 0 for a slot with no token
+        float lt = f * row_group_sum(st.l[set]);
         lt += __shfl_xor(lt, 16, kWave);
         lt += __shfl_xor(lt, 32, kWave);
-        const float zf = f * st.z[set];
+        float zt = f * row_group_sum(st.z[set]);
+        zt += __shfl_xor(zt, 16, kWave);
+        zt += __shfl_xor(zt, 32, kWave);
         const float safe_l = lt > 0.f ? lt : 1.f;
         const float inv = 1.f / safe_l;
-        float *row = mid_o + (((int64_t)b * num_q_heads + kvh * G + 4 * set + c) * num_splits + sid) *
-                                 (kHeadDim + 1);
+        // per-head factors for the accumulator registers (reg h = head h)
+        const float fh[4] = {quad_bcast<0>(f), quad_bcast<1>(f), quad_bcast<2>(f),
+                             quad_bcast<3>(f)};
+        const float zh[4] = {quad_bcast<0>(zt), quad_bcast<1>(zt), quad_bcast<2>(zt),
+                             quad_bcast<3>(zt)};
+        const float ih[4] = {quad_bcast<0>(inv), quad_bcast<1>(inv), quad_bcast<2>(inv),
+                             quad_bcast<3>(inv)};
+        // lane (u,v,c) writes head 4*set + u, dims 32v + 8c .. +7
+        float *row = mid_o +
+                     (((int64_t)b * num_q_heads + kvh * G + 4 * set + u) * num_splits + sid) *
+                         (kHeadDim + 1);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
+            float out = 0.f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float o = f * st.acc[set][k][r] + zf;
+            for (int h = 0; h < 4; ++h) {
+                float o = fh[h] * inv_code_unit * st.acc[set][k][h];
                 o += __shfl_xor(o, 16, kWave);
                 o += __shfl_xor(o, 32, kWave);
-                if (r == u)
-                    row[32 * v + 8 * r + k] = o * inv;
+                if (h == u)
+                    out = (o + zh[h]) * ih[h];
             }
+            row[32 * v + 8 * c + k] = out;
         }
-        if (lane < 4)
-            row[kHeadDim] = mx * kLn2 + logf(safe_l);
+        if (lane < 4) {
+            float *lrow = mid_o + (((int64_t)b * num_q_heads + kvh * G + 4 * set + c) * num_splits +
+                                   sid) * (kHeadDim + 1);
+            lrow[kHeadDim] = mx * kLn2 + logf(safe_l);
+        }
     }
 }
 
