@@ -98,12 +98,16 @@ __device__ __forceinline__ void build_key_table(typename KEntry<LAYOUT>::type *t
     }
 }
 
-// Per-lane byte offsets inside one KV block (fixed for a kernel instance).
+// Per-lane byte offsets inside one KV block (fixed for a kernel instance).  The
+// per-token steps that are the same for every lane (V dword of token 4u+i relative
+// to token 4u, the three SoA metadata arrays) travel in the loads' scalar offsets.
 struct LaneOffsets {
-    uint32_t k;     // K bytes of token 4u + ((c+v) & 3), dims 32v ..
-    uint32_t v[4];  // V dword of token 4u + i, dims 32v + 8c ..
-    uint32_t m;     // SoA: norm of token 4u + v; AoS: slot of token 4u + v
-    uint32_t mf;    // SoA: distance between the three metadata arrays
+    uint32_t k;   // K bytes of token 4u + ((c+v) & 3), dims 32v ..
+    uint32_t v0;  // V dword of token 4u, dims 32v + 8c ..; token 4u+i adds i * tok_stride
+    uint32_t m;   // SoA: norm of token 4u + v; AoS: slot of token 4u + v
+    int tok_stride;  // bytes between consecutive tokens of one kv-head
+    int mf;          // SoA: bytes between the three metadata arrays
+    int v_shift;     // AoS: v0 & 3 (the same in every lane)
 };
 
 template <int LAYOUT>
@@ -112,20 +116,18 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int u, int v, int c, int kvh
     LaneOffsets o;
     const int kt = 4 * u + ((c + v) & 3);
     const int st = 4 * u + v;
+    const int rec = LAYOUT == 0 ? kSoaRecord : kAosSlot;
+    o.tok_stride = hk * rec;
+    o.k = (kt * hk + kvh) * rec + 16 * v;  // AoS: 2-byte aligned
+    o.v0 = (4 * u * hk + kvh) * rec + kHalfD + (LAYOUT == 0 ? 0 : 2) + 16 * v + 4 * c;
     if (LAYOUT == 0) {
-        o.k = (kt * hk + kvh) * kSoaRecord + 16 * v;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            o.v[i] = ((4 * u + i) * hk + kvh) * kSoaRecord + kHalfD + 16 * v + 4 * c;
         o.m = block_size * hk * kSoaRecord + (kvh * 3 * block_size + st) * 2;
         o.mf = block_size * 2;
+        o.v_shift = 0;
     } else {
-        o.k = (kt * hk + kvh) * kAosSlot + 16 * v;  // 2-byte aligned
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            o.v[i] = ((4 * u + i) * hk + kvh) * kAosSlot + kHalfD + 2 + 16 * v + 4 * c;
         o.m = (st * hk + kvh) * kAosSlot;
         o.mf = 0;
+        o.v_shift = (kvh * kAosSlot + kHalfD + 2) & 3;  // lane terms are multiples of 4
     }
     return o;
 }
@@ -159,10 +161,10 @@ __device__ __forceinline__ void issue_tile(RawTile<LAYOUT> &t, __amdgpu_buffer_r
         t.k = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v[i], doff, 0);
+            t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
         t.norm = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff, 0);
-        t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + o.mf, moff, 0);
-        t.zero = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + 2 * o.mf, moff, 0);
+        t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff + o.mf, 0);
+        t.zero = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff + 2 * o.mf, 0);
     } else {
         const uint32_t ka = o.k & ~3u;
         const auto k03 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ka, doff, 0);
@@ -171,10 +173,15 @@ __device__ __forceinline__ void issue_tile(RawTile<LAYOUT> &t, __amdgpu_buffer_r
         t.k[2] = k03[2];
         t.k[3] = k03[3];
         t.k[4] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, ka + 16, doff, 0);
+        // token 4u+i's V dword starts sh = (v_shift + i * tok_stride) & 3 bytes past a
+        // dword; both offsets below are multiples of 4 and non-negative.
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            const int sh = (o.v_shift + i * o.tok_stride) & 3;
             t.v[i] = __builtin_bit_cast(
-                uint2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, o.v[i] & ~3u, doff, 0));
+                uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                           rsrc, o.v0 - o.v_shift, doff + i * o.tok_stride + o.v_shift - sh, 0));
+        }
         t.norm = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHalfD, doff, 0);
         t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHeadDim + 2, doff, 0);
         t.zero = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHeadDim + 4, doff, 0);
@@ -197,7 +204,8 @@ __device__ __forceinline__ TileRegs decode_tile(const RawTile<LAYOUT> &t, const 
         r.k.w = __builtin_amdgcn_alignbyte(t.k[4], t.k[3], sh);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            r.v[i] = __builtin_amdgcn_alignbyte(t.v[i].y, t.v[i].x, o.v[i] & 3u);
+            r.v[i] = __builtin_amdgcn_alignbyte(t.v[i].y, t.v[i].x,
+                                                (o.v_shift + i * o.tok_stride) & 3);
     }
     r.norm = t.norm;
     r.scale = t.scale;
@@ -223,42 +231,55 @@ template <int NSET> struct QOperands {
 // Dots of one tile (one MFMA chain per head set) and, for AoS, the lane's share of
 // ||c[idx]||^2 of its K token.
 template <int NSET> struct TileScores {
-    floatx4 sc[NSET];
+    floatx4 sc[NSET], sd[NSET];  // two independent chains: low / high nibbles
     float csq_part;
 };
 
+// One K code byte b (dims 2b, 2b+1 of the lane's dim group) into the two QK^T chains.
 template <int LAYOUT, int NSET>
-__device__ __forceinline__ void qk_tile(const uint4 &k, const typename KEntry<LAYOUT>::type *ktab,
+__device__ __forceinline__ void qk_byte(int bidx, uint32_t byte, const typename KEntry<LAYOUT>::type *ktab,
                                         const QOperands<NSET> &q, TileScores<NSET> &s) {
+    const auto e = ktab[byte];
+    if constexpr (LAYOUT == 1)
+        s.csq_part += e.z;
 #pragma unroll
-    for (int set = 0; set < NSET; ++set)
-        s.sc[set] = floatx4{0.f, 0.f, 0.f, 0.f};
-    s.csq_part = 0.f;
-    const uint32_t kwords[4] = {k.x, k.y, k.z, k.w};
-#pragma unroll
-    for (int bidx = 0; bidx < 16; ++bidx) {
-        const auto e = ktab[(kwords[bidx >> 2] >> (8 * (bidx & 3))) & 0xFFu];  // dims 2b, 2b+1
-        if constexpr (LAYOUT == 1)
-            s.csq_part += e.z;
-#pragma unroll
-        for (int set = 0; set < NSET; ++set) {
-            // dims 2b and 2b+1 = 4k + g with k = b / 2, g = 2 (b % 2) + {0, 1}
-            if (bidx & 1) {
-                s.sc[set] = mfma_f32_bcast<2>(e.x, q.v[set][bidx >> 1], s.sc[set]);
-                s.sc[set] = mfma_f32_bcast<3>(e.y, q.v[set][bidx >> 1], s.sc[set]);
-            } else {
-                s.sc[set] = mfma_f32_bcast<0>(e.x, q.v[set][bidx >> 1], s.sc[set]);
-                s.sc[set] = mfma_f32_bcast<1>(e.y, q.v[set][bidx >> 1], s.sc[set]);
-            }
+    for (int set = 0; set < NSET; ++set) {
+        // dims 2b and 2b+1 = 4k + g with k = b / 2, g = 2 (b % 2) + {0, 1}
+        if (bidx & 1) {
+            s.sc[set] = mfma_f32_bcast<2>(e.x, q.v[set][bidx >> 1], s.sc[set]);
+            s.sd[set] = mfma_f32_bcast<3>(e.y, q.v[set][bidx >> 1], s.sd[set]);
+        } else {
+            s.sc[set] = mfma_f32_bcast<0>(e.x, q.v[set][bidx >> 1], s.sc[set]);
+            s.sd[set] = mfma_f32_bcast<1>(e.y, q.v[set][bidx >> 1], s.sd[set]);
         }
     }
 }
 
+template <int NSET> __device__ __forceinline__ void clear_scores(TileScores<NSET> &s) {
+#pragma unroll
+    for (int set = 0; set < NSET; ++set) {
+        s.sc[set] = floatx4{0.f, 0.f, 0.f, 0.f};
+        s.sd[set] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    s.csq_part = 0.f;
+}
+
+template <int LAYOUT, int NSET>
+__device__ __forceinline__ void qk_tile(const uint4 &k, const typename KEntry<LAYOUT>::type *ktab,
+                                        const QOperands<NSET> &q, TileScores<NSET> &s) {
+    clear_scores(s);
+    const uint32_t kwords[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+    for (int bidx = 0; bidx < 16; ++bidx)
+        qk_byte<LAYOUT, NSET>(bidx, (kwords[bidx >> 2] >> (8 * (bidx & 3))) & 0xFFu, ktab, q, s);
+}
+
 // Full score of token 4u+v (head c) from the rotated partial dots.
-__device__ __forceinline__ float gather_score(const floatx4 &sc) {
-    float s = sc[0] + dpp<kRor4>(sc[1]);
-    s += dpp<kRor8>(sc[2]);
-    return s + dpp<kRor12>(sc[3]);
+__device__ __forceinline__ float gather_score(const floatx4 &sc, const floatx4 &sd) {
+    const floatx4 t = sc + sd;
+    float s = t[0] + dpp<kRor4>(t[1]);
+    s += dpp<kRor8>(t[2]);
+    return s + dpp<kRor12>(t[3]);
 }
 
 // ||c[idx]||^2 of token 4u+v from the per-lane shares (lane (v', c') holds the share of
@@ -287,7 +308,7 @@ __device__ __forceinline__ void softmax_tile(const TileScores<NSET> &s, const Ti
     }
 #pragma unroll
     for (int set = 0; set < NSET; ++set) {
-        const float dot = gather_score(s.sc[set]);
+        const float dot = gather_score(s.sc[set], s.sd[set]);
         float s2 = fmaf(dot, norm, st.negm[set]);  // score - m
         if (boundary)
             s2 = valid ? s2 : -INFINITY;
@@ -323,35 +344,143 @@ __device__ __forceinline__ void softmax_tile(const TileScores<NSET> &s, const Ti
     }
 }
 
-// PV of one tile on the matrix cores: token 4u+i's weights come from block (u, i).
-template <int NSET>
-__device__ __forceinline__ void pv_tile(const TileRegs &t, const float (&pw)[NSET],
+// V codes of token 4u+i as floats: code[k] = code of dim 32v + 8c + k, times 2^-9.
+__device__ __forceinline__ void v_codes(uint32_t w, float (&code)[8]) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;         // dims 8c + 0, 2, 4, 6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // dims 8c + 1, 3, 5, 7
+    const auto c02 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+    const auto c46 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+    const auto c13 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+    const auto c57 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+    code[0] = c02[0];
+    code[1] = c13[0];
+    code[2] = c02[1];
+    code[3] = c13[1];
+    code[4] = c46[0];
+    code[5] = c57[0];
+    code[6] = c46[1];
+    code[7] = c57[1];
+}
+
+template <int I, int NSET>
+__device__ __forceinline__ void pv_pair(const float (&pw)[NSET], float c0, float c1, int k,
                                         SoftmaxState<NSET> &st) {
 #pragma unroll
+    for (int set = 0; set < NSET; ++set) {
+        st.acc[set][k] = mfma_f32_abcast<I>(pw[set], c0, st.acc[set][k]);
+        st.acc[set][k + 1] = mfma_f32_abcast<I>(pw[set], c1, st.acc[set][k + 1]);
+    }
+}
+
+// PV of the current tile (token 4u+i's weights come from block (u, i)) interleaved
+// with QK^T of the next tile: per K byte, two QK^T MFMAs and two PV MFMAs, so the
+// dependent QK^T chains are spaced by independent PV work.
+template <int LAYOUT, int NSET>
+__device__ __forceinline__ void pv_qk_tile(const TileRegs &t, const float (&pw)[NSET],
+                                           SoftmaxState<NSET> &st, const uint4 &knext,
+                                           const typename KEntry<LAYOUT>::type *ktab,
+                                           const QOperands<NSET> &q, TileScores<NSET> &s) {
+    clear_scores(s);
+    const uint32_t kwords[4] = {knext.x, knext.y, knext.z, knext.w};
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = t.v[i] & 0x0F0F0F0Fu;         // codes of dims 8c + 0, 2, 4, 6
-        const uint32_t hi = (t.v[i] >> 4) & 0x0F0F0F0Fu;  // codes of dims 8c + 1, 3, 5, 7
-        const auto c02 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-        const auto c46 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-        const auto c13 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-        const auto c57 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-        const float code[8] = {c02[0], c13[0], c02[1], c13[1], c46[0], c57[0], c46[1], c57[1]};
+        float code[8];
+        v_codes(t.v[i], code);
 #pragma unroll
-        for (int set = 0; set < NSET; ++set) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                switch (i) {
-                case 0: st.acc[set][k] = mfma_f32_abcast<0>(pw[set], code[k], st.acc[set][k]); break;
-                case 1: st.acc[set][k] = mfma_f32_abcast<1>(pw[set], code[k], st.acc[set][k]); break;
-                case 2: st.acc[set][k] = mfma_f32_abcast<2>(pw[set], code[k], st.acc[set][k]); break;
-                default: st.acc[set][k] = mfma_f32_abcast<3>(pw[set], code[k], st.acc[set][k]); break;
-                }
+        for (int r = 0; r < 4; ++r) {
+            const int bidx = 4 * i + r;
+            qk_byte<LAYOUT, NSET>(bidx, (kwords[i] >> (8 * r)) & 0xFFu, ktab, q, s);
+            switch (i) {
+            case 0: pv_pair<0, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
+            case 1: pv_pair<1, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
+            case 2: pv_pair<2, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
+            default: pv_pair<3, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
             }
         }
     }
 }
 
-template <int LAYOUT, int NSET>
+// Lane-pair exchanges of gfx950 (v_permlane32_swap / v_permlane16_swap).
+__device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float bitsf(uint32_t x) { return __builtin_bit_cast(float, x); }
+// Sum of x over lanes l and l ^ 32 (resp. l ^ 16), in every lane.
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(x), fbits(x), false, false);
+    return bitsf(r[0]) + bitsf(r[1]);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
+    return bitsf(r[0]) + bitsf(r[1]);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(x), fbits(x), false, false);
+    return fmaxf(bitsf(r[0]), bitsf(r[1]));
+}
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
+    return fmaxf(bitsf(r[0]), bitsf(r[1]));
+}
+// Reduce-scatter over lane halves: lanes 0..31 get a[l] + a[l+32], lanes 32..63 get
+// c[l-32] + c[l].
+__device__ __forceinline__ float rs_xor32(float a, float c) {
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(a), fbits(c), false, false);
+    return bitsf(r[0]) + bitsf(r[1]);
+}
+// Same over 16-lane rows: even rows get a summed with the next row, odd rows get c
+// summed with the previous row.
+__device__ __forceinline__ float rs_xor16(float a, float c) {
+    const auto r = __builtin_amdgcn_permlane16_swap(fbits(a), fbits(c), false, false);
+    return bitsf(r[0]) + bitsf(r[1]);
+}
+
+// Merge the four slots u of one split and write its rows: lane (u,v,c) writes head
+// 4*set + u, dims 32v + 8c .. +7, and lanes 0..3 write the LSE of heads 4*set + c.
+template <int NSET>
+__device__ __forceinline__ void write_split(const SoftmaxState<NSET> &st, float *__restrict__ mid_o,
+                                            int64_t row0, int num_splits, int sid, int u, int v,
+                                            int c, int lane, float inv_code_unit) {
+#pragma unroll
+    for (int set = 0; set < NSET; ++set) {
+        // slot (u, head c): max over the slots, then l / z summed over the slot's lanes v
+        // and over the slots with their factors
+        const float m = -st.negm[set];
+        const float mx = max_xor16(max_xor32(m));
+        const float f = __builtin_amdgcn_exp2f(m - mx);  // 0 for a slot with no token
+        const float lt = sum_xor16(sum_xor32(f * row_group_sum(st.l[set])));
+        const float zt = sum_xor16(sum_xor32(f * row_group_sum(st.z[set])));
+        const float safe_l = lt > 0.f ? lt : 1.f;
+        // head c totals -> the lanes that write head u
+        const int src = (lane & ~3) | u;
+        const float z_u = __shfl(zt, src, kWave);
+        const float inv_u = 1.f / __shfl(safe_l, src, kWave);
+        // accumulator register h = head h: scale by slot u's factor for head h
+        const float fh0 = quad_bcast<0>(f) * inv_code_unit, fh1 = quad_bcast<1>(f) * inv_code_unit;
+        const float fh2 = quad_bcast<2>(f) * inv_code_unit, fh3 = quad_bcast<3>(f) * inv_code_unit;
+        float *row = mid_o + ((row0 + 4 * set + u) * num_splits + sid) * (kHeadDim + 1);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const floatx4 a = st.acc[set][k];
+            // sum over slots u: heads 0 / 2 and 1 / 3 split across the lane halves, then
+            // across rows, leaving head u in lane group u
+            const float x = rs_xor32(a[0] * fh0, a[2] * fh2);
+            const float y = rs_xor32(a[1] * fh1, a[3] * fh3);
+            const float o = rs_xor16(x, y);
+            row[32 * v + 8 * c + k] = (o + z_u) * inv_u;
+        }
+        if (lane < 4) {
+            float *lrow = mid_o + ((row0 + 4 * set + c) * num_splits + sid) * (kHeadDim + 1);
+            lrow[kHeadDim] = mx * kLn2 + logf(safe_l);
+        }
+    }
+}
+
+// One wave handles a run of consecutive live splits of one (sequence, kv-head).  Their tiles form one stream: split s contributes n_s tiles padded to a
+// multiple of 4 stream positions (padding positions re-read the split's last tile and
+// mask every token), so split ends fall on 4-stage group boundaries.  The load ring
+// and the QK^T pipeline run across split boundaries; after a split's last group the
+// wave writes its rows and restarts the softmax state (the first rescale of the next
+// split multiplies the old accumulators by 0).  RING tiles are in flight per wave.
+template <int LAYOUT, int NSET, int RING>
 __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
@@ -360,12 +489,20 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
     float score_scale_log2) {
     constexpr int G = 4 * NSET;
     const int block_size = 1 << block_size_log2;
-    const int sid = blockIdx.x;
-    const int kvh = blockIdx.y;
+    // grid (Hk, W, B): the kv-heads of one (sequence, split run) are dispatched together,
+    // so the waves that read the same KV blocks run at about the same time.
+    const int kvh = blockIdx.x;
+    const int wid = blockIdx.y, nw = gridDim.y;
     const int b = blockIdx.z;
     const int lane = threadIdx.x;
-    const SplitRange rng = split_range(seq_lens[b], num_splits, sid);
-    if (rng.start >= rng.end)
+    const int seq_len = seq_lens[b];
+    // split partition: L = ceil(len / S); live splits are those with s * L < len
+    const int split_len = (seq_len + num_splits - 1) / num_splits;
+    // wave x of the W waves of this (sequence, kv-head) takes splits [x * S / W, (x + 1) * S / W)
+    const int s_lo = (int)((int64_t)wid * num_splits / nw);
+    const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
+    const int s_hi = min((int)((int64_t)(wid + 1) * num_splits / nw), live);
+    if (s_lo >= s_hi)
         return;
     const int c = lane & 3;
     const int v = (lane >> 2) & 3;
@@ -396,20 +533,33 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
             st.acc[set][k] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
+    // stream positions of a split with n tiles: n rounded up to a whole ring turn
+    static_assert(RING == 4 || RING == 8, "ring of 4 or 8 tiles");
+    auto ring_padded = [](int n) { return (n + RING - 1) & ~(RING - 1); };
+    int total = 0;
+    for (int s = s_lo; s < s_hi; ++s) {
+        const int st0 = s * split_len, en = min(st0 + split_len, seq_len);
+        total += ring_padded(((en - 1) >> 4) - (st0 >> 4) + 1);
+    }
+
     const LaneOffsets off = lane_offsets<LAYOUT>(u, v, c, kvh, num_kv_heads, block_size);
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
-    const int tile_first = rng.start & ~15;
-    const int ntiles = (((rng.end - 1) & ~15) - tile_first) / 16 + 1;
-    // lane's softmax token relative to the split start, at tile 0
-    const int rel0 = tile_first + 4 * u + v - rng.start;
-    const uint32_t span = (uint32_t)(rng.end - rng.start);
+    const int ktok = 4 * u + v;  // the lane's softmax token within a tile
+    const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
+    const float inv_code_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
     __syncthreads();
 
-    // Issue the loads of tile j (global index) into ring slot r; its block id sits in
-    // lane (j mod 64) of bt_lane_val.
-    auto issue = [&](RawTile<LAYOUT> &r, int bt_lane_val, int j) {
-        const int blk = __builtin_amdgcn_readlane(bt_lane_val, j & 63);
-        const int toff = (tile_first + 16 * j) & (block_size - 1);
+    // current split (uniform): [cur_start, cur_end), stream position of its end
+    int cur = s_lo;
+    int cur_start = cur * split_len;
+    int cur_end = min(cur_start + split_len, seq_len);
+    int cur_stop = ring_padded(((cur_end - 1) >> 4) - (cur_start >> 4) + 1);
+
+    // Issue the loads of stream position j into ring slot r; its block id and tile index
+    // sit in lane (j mod 64) of bt_lane / tile_lane.
+    auto issue = [&](RawTile<LAYOUT> &r, int bt_lane, int tile_lane, int j) {
+        const int blk = __builtin_amdgcn_readlane(bt_lane, j & 63);
+        const int toff = (16 * __builtin_amdgcn_readlane(tile_lane, j & 63)) & (block_size - 1);
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(cache) + (int64_t)blk * block_stride, 0, 0x7FFFFFFF, 0x00020000);
         // The scheduling barriers keep the ring's loads in program order, which is what
@@ -419,98 +569,78 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
                            toff * 2, off);
         __builtin_amdgcn_sched_barrier(0);
     };
-    // Stage j: softmax of tile j (scores computed by the previous stage), then one
-    // branch-free block with PV of tile j and QK^T of tile j+1, so the MFMA streams and
-    // the decode work interleave.  QK^T after the chunk's last tile reads a clamped
-    // (valid) tile and its scores are discarded.
+    // Stage j: softmax of position j (scores computed by the previous stage), then one
+    // branch-free block with PV of position j and QK^T of position j+1, so the MFMA
+    // streams and the decode work interleave.
     TileScores<NSET> sc;
-    auto stage = [&](const RawTile<LAYOUT> &cur, const RawTile<LAYOUT> &nxt, int j) {
-        const TileRegs t = decode_tile<LAYOUT>(cur, off);
-        const int t0 = tile_first + 16 * j;
-        const bool boundary = !(t0 >= rng.start && t0 + 16 <= rng.end);
-        const bool valid = (uint32_t)(rel0 + 16 * j) < span;
+    auto stage = [&](const RawTile<LAYOUT> &cur_t, const RawTile<LAYOUT> &nxt_t, int mask_lane,
+                     int j) {
+        const TileRegs t = decode_tile<LAYOUT>(cur_t, off);
+        const int t0 = 16 * __builtin_amdgcn_readlane(mask_lane, j & 63);
+        const bool boundary = !(t0 >= cur_start && t0 + 16 <= cur_end);
+        const bool valid = (uint32_t)(t0 + ktok - cur_start) < (uint32_t)(cur_end - cur_start);
         float pw[NSET];
         softmax_tile<LAYOUT, NSET>(sc, t, st, pw, boundary, valid);
-        pv_tile<NSET>(t, pw, st);
-        qk_tile<LAYOUT, NSET>(decode_tile<LAYOUT>(nxt, off).k, ktab, q, sc);
+        pv_qk_tile<LAYOUT, NSET>(t, pw, st, decode_tile<LAYOUT>(nxt_t, off).k, ktab, q, sc);
     };
 
-    // Tiles in chunks of 64 (one block-table entry per lane); within a chunk a 4-slot
-    // register ring keeps the loads of the next tiles in flight: each slot is refilled
-    // right after its tile is consumed.  Every ring load and every stage is
-    // unconditional -- past the chunk's last tile a load re-reads that tile (an L2 hit)
-    // and the stage masks all of its tokens -- so all paths issue the same loads in the
-    // same order and each wait counts exactly the loads of later tiles.
-    for (int j0 = 0; j0 < ntiles; j0 += 64) {
-        const int n = min(64, ntiles - j0);
+    // Stream positions in chunks of 64 (one block-table entry per lane); within a chunk
+    // a 4-slot register ring keeps the loads of the next positions in flight: each slot
+    // is refilled right after its tile is consumed.  Every ring load and every stage is
+    // unconditional -- past the chunk's end a load re-reads its last tile (an L2 hit) --
+    // so all paths issue the same loads in the same order and each wait counts exactly
+    // the loads of later positions.
+    int pos_base = 0;  // stream position where split `cur` starts
+    for (int j0 = 0; j0 < total; j0 += 64) {
+        const int n = min(64, total - j0);
         const int last = j0 + n - 1;
-        const int bt_val = bt[(tile_first + 16 * (j0 + min(lane, n - 1))) >> block_size_log2];
-        RawTile<LAYOUT> r0, r1, r2, r3;
-        issue(r0, bt_val, j0);
-        issue(r1, bt_val, min(j0 + 1, last));
-        issue(r2, bt_val, min(j0 + 2, last));
-        issue(r3, bt_val, min(j0 + 3, last));
-        qk_tile<LAYOUT, NSET>(decode_tile<LAYOUT>(r0, off).k, ktab, q, sc);
-        int j = j0;
-        do {
-            stage(r0, r1, j);
-            issue(r0, bt_val, min(j + 4, last));
-            stage(r1, r2, j + 1);
-            issue(r1, bt_val, min(j + 5, last));
-            stage(r2, r3, j + 2);
-            issue(r2, bt_val, min(j + 6, last));
-            stage(r3, r0, j + 3);
-            issue(r3, bt_val, min(j + 7, last));
-            j += 4;
-        } while (j <= last);
-    }
-
-    // ---- merge the four slots u and write this split's rows
-    // fp8 decode factor: a V code n was accumulated as n * code_unit
-    const float inv_code_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
-#pragma unroll
-    for (int set = 0; set < NSET; ++set) {
-        // slot (u, head c): max, and l / z summed over the slot's four lanes v
-        const float m = -st.negm[set];
-        float mx = fmaxf(m, __shfl_xor(m, 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float f = __builtin_amdgcn_exp2f(m - mx);  // 0 for a slot with no token
-        float lt = f * row_group_sum(st.l[set]);
-        lt += __shfl_xor(lt, 16, kWave);
-        lt += __shfl_xor(lt, 32, kWave);
-        float zt = f * row_group_sum(st.z[set]);
-        zt += __shfl_xor(zt, 16, kWave);
-        zt += __shfl_xor(zt, 32, kWave);
-        const float safe_l = lt > 0.f ? lt : 1.f;
-        const float inv = 1.f / safe_l;
-        // per-head factors for the accumulator registers (reg h = head h)
-        const float fh[4] = {quad_bcast<0>(f), quad_bcast<1>(f), quad_bcast<2>(f),
-                             quad_bcast<3>(f)};
-        const float zh[4] = {quad_bcast<0>(zt), quad_bcast<1>(zt), quad_bcast<2>(zt),
-                             quad_bcast<3>(zt)};
-        const float ih[4] = {quad_bcast<0>(inv), quad_bcast<1>(inv), quad_bcast<2>(inv),
-                             quad_bcast<3>(inv)};
-        // lane (u,v,c) writes head 4*set + u, dims 32v + 8c .. +7
-        float *row = mid_o +
-                     (((int64_t)b * num_q_heads + kvh * G + 4 * set + u) * num_splits + sid) *
-                         (kHeadDim + 1);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            float out = 0.f;
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                float o = fh[h] * inv_code_unit * st.acc[set][k][h];
-                o += __shfl_xor(o, 16, kWave);
-                o += __shfl_xor(o, 32, kWave);
-                if (h == u)
-                    out = (o + zh[h]) * ih[h];
+        // lane i: the tile at stream position j0 + i (clamped to the chunk)
+        int tile_lane = 0, mask_lane = 0;
+        {
+            const int p = j0 + min(lane, n - 1);
+            int base = 0;
+            for (int s = s_lo; s < s_hi; ++s) {
+                const int st0 = s * split_len, en = min(st0 + split_len, seq_len);
+                const int tf = st0 >> 4, nt = ((en - 1) >> 4) - tf + 1;
+                if (p >= base) {
+                    const int o = p - base;
+                    tile_lane = tf + min(o, nt - 1);
+                    mask_lane = o < nt ? tile_lane : -(1 << 24);  // padding: no valid token
+                }
+                base += ring_padded(nt);
             }
-            row[32 * v + 8 * c + k] = out;
         }
-        if (lane < 4) {
-            float *lrow = mid_o + (((int64_t)b * num_q_heads + kvh * G + 4 * set + c) * num_splits +
-                                   sid) * (kHeadDim + 1);
-            lrow[kHeadDim] = mx * kLn2 + logf(safe_l);
+        const int bt_lane = bt[(16 * tile_lane) >> block_size_log2];
+        RawTile<LAYOUT> ring[RING];
+#pragma unroll
+        for (int k = 0; k < RING; ++k)
+            issue(ring[k], bt_lane, tile_lane, min(j0 + k, last));
+        qk_tile<LAYOUT, NSET>(decode_tile<LAYOUT>(ring[0], off).k, ktab, q, sc);
+        int j = j0;
+        while (true) {
+            // ring turns up to the end of the current split or of the chunk
+            const int stop = min(pos_base + cur_stop, last + 1);
+            do {
+#pragma unroll
+                for (int k = 0; k < RING; ++k) {
+                    stage(ring[k], ring[(k + 1) % RING], mask_lane, j + k);
+                    issue(ring[k], bt_lane, tile_lane, min(j + k + RING, last));
+                }
+                j += RING;
+            } while (j < stop);
+            if (j == pos_base + cur_stop) {
+                write_split<NSET>(st, mid_o, row0, num_splits, cur, u, v, c, lane, inv_code_unit);
+#pragma unroll
+                for (int set = 0; set < NSET; ++set)
+                    st.negm[set] = __FLT_MAX__;
+                pos_base = j;
+                ++cur;
+                cur_start = cur * split_len;
+                cur_end = min(cur_start + split_len, seq_len);
+                cur_stop = ring_padded(((cur_end - 1) >> 4) - (cur_start >> 4) + 1);
+            }
+            if (j > last)
+                break;
         }
     }
 }

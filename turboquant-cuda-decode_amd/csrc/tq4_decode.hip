@@ -5,6 +5,7 @@
 // baseline/triton_v2.py:594-607, but report through a return code and a thread-local
 // message instead of throwing.
 #include <hip/hip_runtime.h>
+#include <cstdlib>
 
 #include <cstdarg>
 #include <cstdio>
@@ -91,9 +92,48 @@ template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t
                        a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
 
+// Waves per (sequence, kv-head) for the MFMA kernel; wave x takes splits
+// [x * S / W, (x + 1) * S / W).  Consecutive splits in one wave share one load
+// pipeline, which removes per-split start-up latency; W is chosen so the grid fills
+// whole rounds of the waves the GPU holds at the kernel's occupancy.
+// TQ4_STAGE1_WAVES overrides W (a tuning knob; results do not depend on it).
+#ifndef TQ4_STAGE1_RING
+#define TQ4_STAGE1_RING 4
+#endif
+constexpr int kStage1Ring = TQ4_STAGE1_RING;  // tiles in flight per wave
+
+template <int LAYOUT, int NSET> int waves_per_sequence(const Stage1Args &a) {
+    static const int forced = [] {
+        const char *e = getenv("TQ4_STAGE1_WAVES");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced > 0)
+        return forced < a.S ? forced : a.S;
+    static int slots = 0;  // waves the device holds at once for this kernel
+    if (!slots) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void *>(&tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>),
+                tq4::kWave, 0) == hipSuccess &&
+            cus > 0 && per_cu > 0)
+            slots = cus * per_cu;
+        else
+            slots = 256 * 4 * 2;
+    }
+    const int64_t pairs = (int64_t)a.Hk * a.B;
+    // smallest number of whole rounds that gives every pair at least one wave
+    const int64_t rounds = (pairs + slots - 1) / slots;
+    int64_t w = rounds * slots / pairs;
+    if (w < 1)
+        w = 1;
+    return (int)(w < a.S ? w : a.S);
+}
+
 template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_t st) {
-    const dim3 grid(a.S, a.Hk, a.B);
-    hipLaunchKernelGGL((tq4::stage1_mfma_kernel<LAYOUT, NSET>), grid, dim3(tq4::kWave), 0, st,
+    const dim3 grid(a.Hk, waves_per_sequence<LAYOUT, NSET>(a), a.B);
+    hipLaunchKernelGGL((tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>), grid, dim3(tq4::kWave), 0, st,
                        a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk,
                        log2_int(a.bs), a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
