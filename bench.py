@@ -4,7 +4,9 @@ One step = one Stage1 launch over the whole batch of the Qwen3-4B-shaped decode
 workload (B=64, ctx 4096, 32/8 heads, D=128, KV block 16, 32 splits, SoA cache,
 random-permuted block table), inputs resident in HBM.  Each timed launch follows a
 1 GiB read sweep so the ~316 MB working set is not served from the 256 MB
-Infinity Cache (cold cache), and is bracketed by HIP events on the launch stream.
+Infinity Cache (cold cache), and is bracketed by HIP events on the launch stream
+(created without the system-scope release fence, so the interval is the kernel's own
+duration, as rocprofv3 reports it).
 
 Prints ONE JSON line.  ``value`` is achieved HBM GB/s = algorithmic bytes per launch /
 mean launch time; ``roofline`` relates it to MI355X's 8 TB/s; ``cpu_baseline`` is the
@@ -57,6 +59,53 @@ def traffic_from_profile(name: str):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", path.read_text())
     return float(m.group(1)) if m else None
+
+
+class HipEvents:
+    """HIP events recorded on the launch stream, created without the system-scope release
+    fence (hipEventDisableSystemFence), so the interval covers the kernel and not an L2
+    write-back of its output; these intervals match rocprofv3's kernel durations."""
+
+    NO_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self, stream: int):
+        import ctypes
+
+        self.ct = ctypes
+        self.hip = None
+        for name in ("libamdhip64.so.7", "libamdhip64.so"):
+            try:
+                self.hip = ctypes.CDLL(name)  # the runtime torch already loaded
+                break
+            except OSError:
+                continue
+        if self.hip is None:
+            raise RuntimeError("libamdhip64 not found")
+        self.stream = ctypes.c_void_p(stream)
+
+    def pair(self):
+        evs = []
+        for _ in range(2):
+            e = self.ct.c_void_p()
+            rc = self.hip.hipEventCreateWithFlags(self.ct.byref(e), self.ct.c_uint(self.NO_SYSTEM_FENCE))
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            evs.append(e)
+        return evs
+
+    def record(self, e):
+        if self.hip.hipEventRecord(e, self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = self.ct.c_float()
+        if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, *evs):
+        for e in evs:
+            self.hip.hipEventDestroy(e)
 
 
 def cpu_baseline(w, threads: int, repeats: int = 3):
@@ -114,33 +163,38 @@ def main() -> int:
     def launch(layout, kernel):
         ops.stage1(q, caches[layout], bt, sl, lut, mid, layout=layout, kernel=kernel)
 
+    timer = HipEvents(torch.cuda.current_stream(dev).cuda_stream)
+
     def cold_times(layout, kernel, steps, warmup):
         for _ in range(warmup):
             flush.sum()
             launch(layout, kernel)
         torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
+        ev = [timer.pair() for _ in range(steps)]
         for a, b in ev:
             flush.sum()  # 1 GiB read sweep: evicts L2 and the Infinity Cache
-            a.record()
+            timer.record(a)
             launch(layout, kernel)
-            b.record()
+            timer.record(b)
         torch.cuda.synchronize()
-        return [a.elapsed_time(b) for a, b in ev]
+        out = [timer.elapsed_ms(a, b) for a, b in ev]
+        for a, b in ev:
+            timer.destroy(a, b)
+        return out
 
     def warm_time(layout, kernel, iters=100, rounds=5):
         res = []
+        a, b = timer.pair()
         for _ in range(rounds):
             for _ in range(10):
                 launch(layout, kernel)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
+            timer.record(a)
             for _ in range(iters):
                 launch(layout, kernel)
-            b.record()
+            timer.record(b)
             torch.cuda.synchronize()
-            res.append(a.elapsed_time(b) / iters)
+            res.append(timer.elapsed_ms(a, b) / iters)
+        timer.destroy(a, b)
         return statistics.median(res)
 
     torch.cuda.synchronize()
