@@ -8,7 +8,7 @@ from . import codebook, layout, workloads  # noqa: F401  (host-side, no GPU need
 __all__ = [
     "codebook", "layout", "workloads", "ops", "stage1", "stage2", "full_decode",
     "rotate_query", "pair_lut_device", "launch_tq4_v2_stage1", "launch_soa_v1_stage1",
-    "launch_aos_v1_stage1", "launch_stage2", "ext", "DecodeWorkspace",
+    "launch_aos_v1_stage1", "launch_stage2", "ext", "DecodeWorkspace", "Tq4Error",
 ]
 
 

@@ -23,6 +23,7 @@ import math
 import torch
 
 from . import _lib
+from ._lib import Tq4Error  # noqa: F401  (raised by every wrapper)
 from .layout import AOS, LAYOUTS, SOA, slot_bytes
 
 KERNELS = {"auto": 0, "simple": 1, "mfma": 2}
