@@ -1,46 +1,51 @@
-// Stage1, matrix-core kernel (gfx950): one wave64 per (split, kv-head, sequence),
-// GQA group G = 4 * NSET, 16-token tiles aligned to the KV block.
+// Stage1, matrix-core kernel (gfx950): one wave64 per run of splits of one (kv-head,
+// sequence), GQA group G = 4 * NSET, 16-token tiles aligned to the KV block.
 //
 // Lane l = 16u + 4v + c (u, v, c in 0..3).  MFMA block = l / 4 = 4u + v, in-block
-// index = c.  All products run on v_mfma_f32_4x4x1f32 (fp32 operands, 16 blocks); its
-// 4x4 shape puts 4 tokens or 4 dims against the 4 heads of a head set, so the GQA
-// group costs no padding.  On gfx950 vector instructions do not overlap fp32 MFMAs,
-// so the layout is chosen to keep the vector work per tile small.
+// index = c.  Products run on v_mfma_f32_4x4x4f16 (16 blocks of 4x4, K = 4, fp32
+// accumulate); the 4x4 shape puts 4 tokens or 4 dims against the 4 heads of a head set,
+// so the GQA group costs no padding.  fp32 accuracy comes from splitting each fp32
+// factor into f16 hi + lo parts (x = hi + lo to ~2^-22): every product of interest is
+// formed from its parts in the MFMA's K dimension.  (On gfx950 vector instructions do
+// not issue while an fp32 MFMA runs; f16 MFMAs leave room for them.)
 //
 // QK^T of a tile (tokens 4u .. 4u+3 in lane group u):
 //   lane (u,v,c) loads the 16 K code bytes of token 4u + ((c + v) & 3), dims 32v ..
-//   32v+31.  A[block (u,v)][row i] = K[4u + ((i + v) & 3)][32v + s] (lane (u,v,i)),
-//   B[block][col j] = q[head j][32v + s], broadcast from lane group s % 4 by the
-//   B lane-group pattern (blgp = 4 + s % 4): lane (g,v,c) holds q[c][32v + 4k + g] in
-//   register k.  32 MFMAs (one per dim of the group) leave in lane (u,v,c) register i
-//   the dot over dim group v of token 4u + ((i + v) & 3) with head c.  The centroids
-//   come from a 256-entry LDS table indexed by the packed code byte (entry = (c[low
-//   nibble], c[high nibble])): one ds_read_b64 gives the A operands of two MFMAs.
-//   Because of the rotation, register k of lane (u, v-k, c) holds token 4u+v's dot
-//   over group v-k, so three DPP row rotations (by 4, 8, 12 lanes) sum the full score
-//   of token 4u + v, head c into lane (u,v,c): one score per lane, no duplicates.
+//   32v+31.  Per code byte b (dims d = 32v+2b, d' = d+1) two MFMAs:
+//     A[block (u,v)][row i][k] = (c_hi[d], c_hi[d'], c_lo[d], c_lo[d'])  of token
+//       4u + ((i + v) & 3) (lane (u,v,i)) -- one ds_read_b64 of a 256-entry LDS table
+//       indexed by the packed byte;
+//     B[k][col j] = (q_hi[d], q_hi[d'], q_hi[d], q_hi[d']) resp. the q_lo parts of head
+//       j, broadcast from lane group b % 4 by the B lane-group pattern (blgp = 4 + b%4):
+//       lane (g,v,c) holds q[c][32v + 8k + 2g, +1] for k = 0..3;
+//   so sum_k A B = c[d] q[d] + c[d'] q[d'] (hi and lo chains accumulate separately).
+//   After 32 MFMAs lane (u,v,c) register i holds the dot over dim group v of token
+//   4u + ((i + v) & 3) with head c.  Because of the rotation, register k of lane
+//   (u, v-k, c) holds token 4u+v's dot over group v-k, so three DPP row rotations (by 4,
+//   8, 12 lanes) sum the full score of token 4u + v, head c into lane (u,v,c): one score
+//   per lane, no duplicates.
 // Softmax: lane (u,v,c) owns token 4u+v, head c.  Slot (u, c) (four lanes v) keeps a
 //   running max m; the max only moves when a score exceeds it by more than
 //   kRescaleLog2 (p <= 2^8), so the rescale branch is rare after a slot's first tile.
 //   Each lane accumulates its own l and z (z = sum p * V zero); slots merge at the end.
-// PV of the tile, step i (token 4u + i), 8 MFMAs k = 0..7:
-//   A[block (u,v)][row h] = p[head h][4u + i] * V scale   -- the A operand of block
-//     (u, i), broadcast to the four blocks of lane group u (cbsz = 2, abid = i), i.e.
-//     exactly where the softmax left it;
-//   B[block (u,v)][col j] = code[4u + i][32v + 8j + k]    -- lane (u,v,j) loads the V
-//     dword of token 4u+i at dims 32v + 8j .. +7;
-//   result lane (u,v,j) reg h += O[head h][32v + 8j + k] (32 accumulators per set).
-//   V codes are converted two at a time with v_cvt_pk_f32_fp8: a byte n < 16 read as
-//   fp8 (e4m3) is exactly n * 2^-9; the power-of-two factor is undone at the end.
+// PV of the tile, per dim k of the lane (dims 32v + 8c + k), two MFMAs (hi, lo):
+//   A[block (u,v)][row h][t] = w_hi[head h][token 4u+t] (resp. w_lo), w = p * V scale --
+//     the A operand of block (u, 3), broadcast to the four blocks of lane group u
+//     (cbsz = 2, abid = 3); lane (u,3,h) gathers the four tokens' w with DPP rotations;
+//   B[t][col j] = code[4u + t][32v + 8j + k] as an f16 bit pattern (the denormal
+//     code * 2^-24; one v_perm_b32 packs two tokens' codes), lane (u,v,j) having loaded
+//     the V dword of each token 4u+t at dims 32v + 8j .. +7;
+//   result lane (u,v,j) reg h += O[head h][32v + 8j + k] * 2^-24 (32 accumulators / set).
+//   w < 65504 is required: p <= 2^8 and V scale < 255.
 //
 // Schedule: stage j = softmax of tile j, then PV of tile j together with QK^T of tile
 // j+1 in one branch-free block (software pipelining across tiles).
 //
 // Memory: the block-table entries of up to 64 tiles are read once (one lane per tile)
-// and broadcast with readlane.  A 4-slot register ring keeps the loads of the next
-// tiles in flight.  Loads are buffer loads off a per-tile descriptor whose base is the
-// KV block (offsets are per-lane constants), plain and unconditional, so the
-// compiler's wait before each tile is exact.
+// and broadcast with readlane.  A register ring keeps the loads of the next tiles in
+// flight.  Loads are buffer loads off a per-tile descriptor whose base is the KV block
+// (offsets are per-lane constants), plain and unconditional, so the compiler's wait
+// before each tile is exact.
 #pragma once
 #include "tq4_device.h"
 
@@ -69,20 +74,33 @@ template <int Q> __device__ __forceinline__ float quad_bcast(float x) {
     return dpp<(Q | (Q << 2) | (Q << 4) | (Q << 6))>(x);
 }
 
+typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ halfx4 as_halfx4(uint32_t lo, uint32_t hi) {
+    return __builtin_bit_cast(halfx4, uint2{lo, hi});
+}
 // B taken from lane group G (lanes 16G .. 16G+15) for all four groups.
-template <int G> __device__ __forceinline__ floatx4 mfma_f32_bcast(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 4 + G);
+template <int G> __device__ __forceinline__ floatx4 mfma_f16_bcast(halfx4 a, halfx4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 4 + G);
 }
 // A taken from block I of each lane group (cbsz = 2, abid = I).
-template <int I> __device__ __forceinline__ floatx4 mfma_f32_abcast(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 2, I, 0);
+template <int I> __device__ __forceinline__ floatx4 mfma_f16_abcast(halfx4 a, halfx4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 2, I, 0);
+}
+// f16 hi + lo parts of an fp32 value, packed (hi in bits 0..15, lo in 16..31); both
+// parts are rounded toward zero, hi + lo = x to ~2^-20 relative.
+__device__ __forceinline__ uint32_t split_f16(float x) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(x, 0.f);
+    const float r = x - (float)h[0];
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, r));
 }
 
-// K-code table entry for one packed byte (low nibble = even dim, high nibble = odd
-// dim): SoA (c[lo], c[hi]); AoS adds c[lo]^2 + c[hi]^2 for the norm correction.
+// K-code table entry for one packed byte (low nibble = even dim d, high nibble = odd
+// dim d'): the f16 parts (c_hi[lo], c_hi[hi], c_lo[lo], c_lo[hi]) -- the A operand of
+// both QK^T MFMAs of the byte; AoS adds c[lo]^2 + c[hi]^2 (fp32) for the norm
+// correction.
 template <int LAYOUT> struct KEntry;
-template <> struct KEntry<0> { typedef float2 type; };
-template <> struct KEntry<1> { typedef float4 type; };
+template <> struct KEntry<0> { typedef uint2 type; };
+template <> struct KEntry<1> { typedef uint4 type; };
 
 template <int LAYOUT>
 __device__ __forceinline__ void build_key_table(typename KEntry<LAYOUT>::type *tbl,
@@ -91,10 +109,13 @@ __device__ __forceinline__ void build_key_table(typename KEntry<LAYOUT>::type *t
         const int lo = e & 15, hi = e >> 4;
         const float c_lo = pair_lut[2 * (lo * 16 + hi)];      // row (lo, hi) = (c[lo], c[hi])
         const float c_hi = pair_lut[2 * (lo * 16 + hi) + 1];
+        const uint32_t p_lo = split_f16(c_lo), p_hi = split_f16(c_hi);
+        const uint32_t his = (p_lo & 0xFFFFu) | (p_hi << 16);   // (c_hi[lo], c_hi[hi])
+        const uint32_t los = (p_lo >> 16) | (p_hi & 0xFFFF0000u);  // (c_lo[lo], c_lo[hi])
         if constexpr (LAYOUT == 0)
-            tbl[e] = make_float2(c_lo, c_hi);
+            tbl[e] = uint2{his, los};
         else
-            tbl[e] = make_float4(c_lo, c_hi, c_lo * c_lo + c_hi * c_hi, 0.f);
+            tbl[e] = uint4{his, los, __builtin_bit_cast(uint32_t, c_lo * c_lo + c_hi * c_hi), 0u};
     }
 }
 
@@ -223,9 +244,11 @@ template <int NSET> struct SoftmaxState {
     floatx4 acc[NSET][8];
 };
 
-// q in the exp2 domain: lane (g,v,c) holds q[head 4*set + c][32v + 4k + g] in v[set][k].
+// q in the exp2 domain as B operands: lane (g,v,c), head 4*set + c, dims
+// d = 32v + 8k + 2g and d+1: hi[set][k] = (q_hi[d], q_hi[d+1], q_hi[d], q_hi[d+1]),
+// lo[set][k] the same with the lo parts.
 template <int NSET> struct QOperands {
-    float v[NSET][8];
+    halfx4 hi[NSET][4], lo[NSET][4];
 };
 
 // Dots of one tile (one MFMA chain per head set) and, for AoS, the lane's share of
@@ -240,17 +263,29 @@ template <int LAYOUT, int NSET>
 __device__ __forceinline__ void qk_byte(int bidx, uint32_t byte, const typename KEntry<LAYOUT>::type *ktab,
                                         const QOperands<NSET> &q, TileScores<NSET> &s) {
     const auto e = ktab[byte];
+    const halfx4 a = as_halfx4(e.x, e.y);
     if constexpr (LAYOUT == 1)
-        s.csq_part += e.z;
+        s.csq_part += __builtin_bit_cast(float, e.z);
 #pragma unroll
     for (int set = 0; set < NSET; ++set) {
-        // dims 2b and 2b+1 = 4k + g with k = b / 2, g = 2 (b % 2) + {0, 1}
-        if (bidx & 1) {
-            s.sc[set] = mfma_f32_bcast<2>(e.x, q.v[set][bidx >> 1], s.sc[set]);
-            s.sd[set] = mfma_f32_bcast<3>(e.y, q.v[set][bidx >> 1], s.sd[set]);
-        } else {
-            s.sc[set] = mfma_f32_bcast<0>(e.x, q.v[set][bidx >> 1], s.sc[set]);
-            s.sd[set] = mfma_f32_bcast<1>(e.y, q.v[set][bidx >> 1], s.sd[set]);
+        // dims 2b, 2b+1 = 8k + 2g (+1) with k = b / 4, g = b % 4
+        switch (bidx & 3) {
+        case 0:
+            s.sc[set] = mfma_f16_bcast<0>(a, q.hi[set][bidx >> 2], s.sc[set]);
+            s.sd[set] = mfma_f16_bcast<0>(a, q.lo[set][bidx >> 2], s.sd[set]);
+            break;
+        case 1:
+            s.sc[set] = mfma_f16_bcast<1>(a, q.hi[set][bidx >> 2], s.sc[set]);
+            s.sd[set] = mfma_f16_bcast<1>(a, q.lo[set][bidx >> 2], s.sd[set]);
+            break;
+        case 2:
+            s.sc[set] = mfma_f16_bcast<2>(a, q.hi[set][bidx >> 2], s.sc[set]);
+            s.sd[set] = mfma_f16_bcast<2>(a, q.lo[set][bidx >> 2], s.sd[set]);
+            break;
+        default:
+            s.sc[set] = mfma_f16_bcast<3>(a, q.hi[set][bidx >> 2], s.sc[set]);
+            s.sd[set] = mfma_f16_bcast<3>(a, q.lo[set][bidx >> 2], s.sd[set]);
+            break;
         }
     }
 }
@@ -344,59 +379,55 @@ __device__ __forceinline__ void softmax_tile(const TileScores<NSET> &s, const Ti
     }
 }
 
-// V codes of token 4u+i as floats: code[k] = code of dim 32v + 8c + k, times 2^-9.
-__device__ __forceinline__ void v_codes(uint32_t w, float (&code)[8]) {
-    const uint32_t lo = w & 0x0F0F0F0Fu;         // dims 8c + 0, 2, 4, 6
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // dims 8c + 1, 3, 5, 7
-    const auto c02 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-    const auto c46 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-    const auto c13 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-    const auto c57 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-    code[0] = c02[0];
-    code[1] = c13[0];
-    code[2] = c02[1];
-    code[3] = c13[1];
-    code[4] = c46[0];
-    code[5] = c57[0];
-    code[6] = c46[1];
-    code[7] = c57[1];
+template <int CTRL> __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, true);
 }
 
-template <int I, int NSET>
-__device__ __forceinline__ void pv_pair(const float (&pw)[NSET], float c0, float c1, int k,
-                                        SoftmaxState<NSET> &st) {
-#pragma unroll
-    for (int set = 0; set < NSET; ++set) {
-        st.acc[set][k] = mfma_f32_abcast<I>(pw[set], c0, st.acc[set][k]);
-        st.acc[set][k + 1] = mfma_f32_abcast<I>(pw[set], c1, st.acc[set][k + 1]);
-    }
+// PV A operands of one head set: the hi / lo f16 parts of w = p * V scale of tokens
+// 4u .. 4u+3 (lane (u,3,h) -- block (u,3) -- is the one the MFMAs read).
+__device__ __forceinline__ void pv_weights(float w, halfx4 &a_hi, halfx4 &a_lo) {
+    const uint32_t t3 = split_f16(w);           // own token 4u+v (v = 3 in block (u,3))
+    const uint32_t t2 = dpp_u32<kRor4>(t3);     // token 4u+v-1
+    const uint32_t t1 = dpp_u32<kRor8>(t3);
+    const uint32_t t0 = dpp_u32<kRor12>(t3);
+    a_hi = as_halfx4(__builtin_amdgcn_perm(t1, t0, 0x05040100u), __builtin_amdgcn_perm(t3, t2, 0x05040100u));
+    a_lo = as_halfx4(__builtin_amdgcn_perm(t1, t0, 0x07060302u), __builtin_amdgcn_perm(t3, t2, 0x07060302u));
 }
 
-// PV of the current tile (token 4u+i's weights come from block (u, i)) interleaved
-// with QK^T of the next tile: per K byte, two QK^T MFMAs and two PV MFMAs, so the
-// dependent QK^T chains are spaced by independent PV work.
+// PV of the current tile interleaved with QK^T of the next tile: per K byte two QK^T
+// MFMAs and one PV MFMA (dim k = b / 2; hi part for even b, lo part for odd b), so the
+// dependent chains are spaced by independent work.
 template <int LAYOUT, int NSET>
 __device__ __forceinline__ void pv_qk_tile(const TileRegs &t, const float (&pw)[NSET],
                                            SoftmaxState<NSET> &st, const uint4 &knext,
                                            const typename KEntry<LAYOUT>::type *ktab,
                                            const QOperands<NSET> &q, TileScores<NSET> &s) {
-    clear_scores(s);
-    const uint32_t kwords[4] = {knext.x, knext.y, knext.z, knext.w};
+    halfx4 a_hi[NSET], a_lo[NSET];
+#pragma unroll
+    for (int set = 0; set < NSET; ++set)
+        pv_weights(pw[set], a_hi[set], a_lo[set]);
+    // codes of the even (low nibble) and odd (high nibble) dims of tokens 4u+i
+    uint32_t even[4], odd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float code[8];
-        v_codes(t.v[i], code);
+        even[i] = t.v[i] & 0x0F0F0F0Fu;
+        odd[i] = (t.v[i] >> 4) & 0x0F0F0F0Fu;
+    }
+    clear_scores(s);
+    const uint32_t kwords[4] = {knext.x, knext.y, knext.z, knext.w};
+    halfx4 codes;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int bidx = 4 * i + r;
-            qk_byte<LAYOUT, NSET>(bidx, (kwords[i] >> (8 * r)) & 0xFFu, ktab, q, s);
-            switch (i) {
-            case 0: pv_pair<0, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
-            case 1: pv_pair<1, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
-            case 2: pv_pair<2, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
-            default: pv_pair<3, NSET>(pw, code[2 * r], code[2 * r + 1], 2 * r, st); break;
-            }
+    for (int bidx = 0; bidx < 16; ++bidx) {
+        qk_byte<LAYOUT, NSET>(bidx, (kwords[bidx >> 2] >> (8 * (bidx & 3))) & 0xFFu, ktab, q, s);
+        const int k = bidx >> 1;  // dim 32v + 8c + k: byte k / 2 of the dword, nibble k % 2
+        if ((bidx & 1) == 0) {
+            const uint32_t sel = (uint32_t)(k >> 1) | 0x0C00u | ((uint32_t)(4 + (k >> 1)) << 16) | 0x0C000000u;
+            const uint32_t *m = (k & 1) ? odd : even;
+            codes = as_halfx4(__builtin_amdgcn_perm(m[1], m[0], sel), __builtin_amdgcn_perm(m[3], m[2], sel));
         }
+#pragma unroll
+        for (int set = 0; set < NSET; ++set)
+            st.acc[set][k] = mfma_f16_abcast<3>((bidx & 1) ? a_lo[set] : a_hi[set], codes, st.acc[set][k]);
     }
 }
 
@@ -511,15 +542,20 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
     __shared__ typename KEntry<LAYOUT>::type ktab[256];
     build_key_table<LAYOUT>(ktab, pair_lut, lane);
 
-    // q of heads (kvh*G + 4*set + c), dims 32v + 4k + u, scaled to the exp2 domain
+    // q of heads (kvh*G + 4*set + c), dims 32v + 8k + 2u (+1), scaled to the exp2 domain
     QOperands<NSET> q;
 #pragma unroll
     for (int set = 0; set < NSET; ++set) {
         const float *qp =
-            q_rot + ((int64_t)b * num_q_heads + kvh * G + 4 * set + c) * kHeadDim + 32 * v + u;
+            q_rot + ((int64_t)b * num_q_heads + kvh * G + 4 * set + c) * kHeadDim + 32 * v + 2 * u;
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            q.v[set][k] = qp[4 * k] * score_scale_log2;
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t p0 = split_f16(qp[8 * k] * score_scale_log2);
+            const uint32_t p1 = split_f16(qp[8 * k + 1] * score_scale_log2);
+            const uint32_t his = (p0 & 0xFFFFu) | (p1 << 16), los = (p0 >> 16) | (p1 & 0xFFFF0000u);
+            q.hi[set][k] = as_halfx4(his, his);
+            q.lo[set][k] = as_halfx4(los, los);
+        }
     }
 
     SoftmaxState<NSET> st;
@@ -546,7 +582,7 @@ __global__ __launch_bounds__(kWave) void stage1_mfma_kernel(
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
     const int ktok = 4 * u + v;  // the lane's softmax token within a tile
     const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
-    const float inv_code_unit = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+    const float inv_code_unit = 16777216.0f;  // V codes enter the MFMA as n * 2^-24
     __syncthreads();
 
     // current split (uniform): [cur_start, cur_end), stream position of its end
