@@ -132,7 +132,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layout", default="soa", choices=["soa", "aos"])
-    ap.add_argument("--kernel", default="auto", choices=["auto", "mfma", "simple"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "mfma", "simple", "xdl"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-variants", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -31,7 +31,12 @@ typedef struct ihipStream_t *tq4_stream_t; /* same type as hipStream_t */
 
 enum tq4_layout { TQ4_LAYOUT_SOA = 0, TQ4_LAYOUT_AOS = 1 };
 enum tq4_dtype { TQ4_F32 = 0, TQ4_BF16 = 1, TQ4_F16 = 2 };
-enum tq4_kernel { TQ4_KERNEL_AUTO = 0, TQ4_KERNEL_SIMPLE = 1, TQ4_KERNEL_MFMA = 2 };
+enum tq4_kernel {
+    TQ4_KERNEL_AUTO = 0,
+    TQ4_KERNEL_SIMPLE = 1,
+    TQ4_KERNEL_MFMA = 2,
+    TQ4_KERNEL_XDL = 3
+};
 enum tq4_status {
     TQ4_OK = 0,
     TQ4_E_INVALID = 1,     /* a shape, pointer or alignment argument is invalid   */
@@ -58,9 +63,10 @@ int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block
                tq4_stream_t stream);
 
 /* Same as tq4_stage1 with an explicit kernel choice (TQ4_KERNEL_*): SIMPLE is the
- * plain-VALU kernel (any GQA group up to 16), MFMA the matrix-core kernel (GQA
- * group 4 or 8, block_size a power of two >= 16, cache_block_stride a multiple of
- * 16).  AUTO picks MFMA when it applies.
+ * plain-VALU kernel (any GQA group up to 16); MFMA (v_mfma_f32_4x4x4_16b_f16) and XDL
+ * (v_mfma_f32_16x16x32_f16) are the matrix-core kernels (GQA group 4 or 8, block_size a
+ * power of two >= 16, cache_block_stride a multiple of 16).  AUTO picks XDL for SoA and
+ * MFMA for AoS caches when they apply, SIMPLE otherwise.
  * Replaces: the per-version entry points tq4_cuda_v1 .. tq4_cuda_v9 (cuda/tq4_cuda_vN_bind.cpp). */
 int tq4_stage1_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
                   const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,

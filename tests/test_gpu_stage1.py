@@ -38,7 +38,7 @@ def assert_parity(got, ref, tol=TOL):
     assert err <= tol, f"max-abs {err} > {tol}"
 
 
-@pytest.mark.parametrize("kernel", ["simple", "mfma"])
+@pytest.mark.parametrize("kernel", ["simple", "mfma", "xdl"])
 @pytest.mark.parametrize("layout", ["soa", "aos"])
 def test_store_fixture_b2_ctx256(config1, dev, kernel, layout):
     f = config1
@@ -49,7 +49,7 @@ def test_store_fixture_b2_ctx256(config1, dev, kernel, layout):
     assert_parity(got, f[f"mid_{layout}"])
 
 
-@pytest.mark.parametrize("kernel", ["simple", "mfma"])
+@pytest.mark.parametrize("kernel", ["simple", "mfma", "xdl"])
 @pytest.mark.parametrize("layout", ["soa", "aos"])
 def test_ragged_with_empty_and_partial_splits(dev, kernel, layout):
     w = workloads.small(101, 6, [1, 3, 17, 100, 257, 999], 32)
@@ -59,14 +59,14 @@ def test_ragged_with_empty_and_partial_splits(dev, kernel, layout):
 
 @pytest.mark.parametrize("kernel,group", [("simple", 1), ("simple", 2), ("simple", 4),
                                           ("simple", 8), ("simple", 16), ("mfma", 4),
-                                          ("mfma", 8)])
+                                          ("mfma", 8), ("xdl", 4), ("xdl", 8)])
 def test_gqa_groups(dev, kernel, group):
     hk = 4
     w = workloads.small(102, 3, [77, 300, 1024], 7, num_q_heads=hk * group, num_kv_heads=hk)
     assert_parity(run(w, dev, kernel), oracle(w))
 
 
-@pytest.mark.parametrize("kernel", ["simple", "mfma"])
+@pytest.mark.parametrize("kernel", ["simple", "mfma", "xdl"])
 @pytest.mark.parametrize("bs", [32, 64])
 def test_larger_kv_blocks(dev, kernel, bs):
     w = workloads.small(103, 3, [130, 511, 64], 5, block_size=bs)
@@ -80,6 +80,7 @@ def test_large_scores_rescale_path(dev):
     w = workloads.small(104, 2, [640, 333], 3)
     w.q_rot = (w.q_rot * 40).astype(np.float32)
     assert_parity(run(w, dev, "mfma"), oracle(w))
+    assert_parity(run(w, dev, "xdl"), oracle(w))
     assert_parity(run(w, dev, "simple"), oracle(w))
 
 
@@ -95,6 +96,18 @@ def test_qwen3_4b_b64_ctx4096_full_size(qwen, dev, layout):
     cache = aos if layout == "aos" else None
     ref = oracle(w, layout, cache)
     assert_parity(run(w, dev, "auto", layout, cache), ref)
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_xdl_qwen3_4b_b64_ctx4096_full_size(qwen, dev, layout):
+    w, aos = qwen
+    cache = aos if layout == "aos" else None
+    assert_parity(run(w, dev, "xdl", layout, cache), oracle(w, layout, cache))
+
+
+def test_xdl_ragged_and_gqa8_full_size(dev):
+    for w in (workloads.ragged_b64(), workloads.gqa8_b8_ctx32768()):
+        assert_parity(run(w, dev, "xdl"), oracle(w))
 
 
 def test_mfma_and_simple_agree_full_size(qwen, dev):

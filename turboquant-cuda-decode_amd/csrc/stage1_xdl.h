@@ -1,0 +1,774 @@
+// Stage1 on gfx950's full-rate f16 matrix instruction v_mfma_f32_16x16x32_f16: one
+// wave64 per run of splits of one (kv-head, sequence), GQA group G = 4 or 8, 16-token
+// tiles aligned to the KV block.
+//
+// Lane l = 16g + n (g = l / 16 in 0..3, n = l % 16).  For a 16x16x32 MFMA, lane (n, g)
+// holds A[row n][k-slots 8g .. 8g+7], B[k-slots 8g .. 8g+7][col n], and D[rows 4g .. 4g+3]
+// [col n].  fp32 accuracy comes from splitting each fp32 factor into f16 hi + lo parts
+// (x = hi + lo to ~2^-20); the parts are placed so that every cross product that
+// matters is formed.
+//
+// Columns / rows that stand for heads: index n -> head n & (G-1), part n >> 3 (0 = hi,
+// 1 = lo).  For G = 4 indices 4..7 and 12..15 repeat 0..3 and 8..11.
+//
+// QK^T of a tile (16 tokens):  lane (n, g) loads token n's 16 code bytes 16g .. 16g+15
+//   (dims 32g ..) in one dwordx4; each byte gives (c_hi[lo], c_hi[hi], c_lo[lo],
+//   c_lo[hi]) through one ds_read_b64 of a 256-entry LDS table.  MFMA m = 0..7 takes
+//   bytes 2m, 2m+1: A[token n][slots] = (c_hi, c_hi, c_lo, c_lo) of each byte's two dims,
+//   B[slots][col] = q_part(col)[head(col)] of the same dims (pre-scaled by attn_scale *
+//   log2 e), so D[t][col] = sum over dims of (c_hi + c_lo) q_part.  Adding column n ^ 8
+//   (DPP row_ror:8) gives the full dot of token 4g + i, head n & (G-1) in register i of
+//   every lane.
+// Softmax: lane (n, g) owns TPL = G / 4 tokens: 4g + TPL * (n / G) + j, head n & (G-1).
+//   The running max m is shared by all lanes of a head and moves only when a score
+//   exceeds it by more than kRescaleLogX (p <= 2^8); that branch is rare after a
+//   split's first tile.  Each lane accumulates its own l = sum p and z = sum p * V zero.
+// PV of a pair of tiles (32 tokens):  A[row][slot s] = w_part(row)[head(row)] of token
+//   4g + (s & 3) of tile s / 4, w = p * V scale (gathered from the owning lanes with DPP
+//   row rotations);  B[slot s][col n] = V code of the same token at dim 8n + j for MFMA
+//   j = 0..7, as an f16 bit pattern (lane (n, g) loads V dword n of tokens 4g .. 4g+3;
+//   v_perm_b32 packs two tokens' bytes).  Accumulator 2m takes the low nibbles (dim
+//   8n + 2m), accumulator 2m + 1 the whole bytes (dim 8n + 2m plus 16 x dim 8n + 2m + 1);
+//   D rows 4g + r hold part g >> 1 of the sums, in units of 2^-24.
+//
+// Schedule: stage t = softmax of tile t, then QK^T of tile t + 1; odd stages also run
+// the PV of tiles (t-1, t), interleaved with that QK^T.  K loads run 4 tiles ahead of
+// their QK^T, V / metadata loads 3-4 tiles ahead of their softmax.
+#pragma once
+#include "tq4_device.h"
+
+namespace tq4 {
+namespace xdl {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+constexpr float kRescaleLogX = 8.0f;
+constexpr int kRor4 = 0x124, kRor8 = 0x128, kRor12 = 0x12C;  // DPP row_ror:N
+
+// DPP row_ror:N -- lane r of a 16-lane row reads lane (r - N) mod 16.
+template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL> __device__ __forceinline__ float dppf(float x) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(uint32_t, x)));
+}
+// Value of quad lane Q broadcast to the whole quad.
+template <int Q> __device__ __forceinline__ float quad_bcast(float x) {
+    return dppf<(Q | (Q << 2) | (Q << 4) | (Q << 6))>(x);
+}
+__device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float bitsf(uint32_t x) { return __builtin_bit_cast(float, x); }
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(x), fbits(x), false, false);
+    return bitsf(r[0]) + bitsf(r[1]);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
+    return bitsf(r[0]) + bitsf(r[1]);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(x), fbits(x), false, false);
+    return fmaxf(bitsf(r[0]), bitsf(r[1]));
+}
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
+    return fmaxf(bitsf(r[0]), bitsf(r[1]));
+}
+// Reduce-scatter over lane halves: lanes 0..31 get a[l] + a[l+32], lanes 32..63 get
+// c[l-32] + c[l].
+__device__ __forceinline__ float rs_xor32(float a, float c) {
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(a), fbits(c), false, false);
+    return bitsf(r[0]) + bitsf(r[1]);
+}
+
+// f16 hi + lo parts of an fp32 value, packed (hi in bits 0..15, lo in 16..31), both
+// rounded toward zero: hi + lo = x to ~2^-20 relative.
+__device__ __forceinline__ uint32_t split_f16(float x) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(x, 0.f);
+    const float r = x - (float)h[0];
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, r));
+}
+__device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(half8, uint4{a, b, c, d});
+}
+__device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// x *= a in x's own register (a tied operand), so that a rarely taken rescale does not
+// give the accumulators new registers that the common path would have to copy into.
+__device__ __forceinline__ void scale_in_place(floatx4 &x, float a0, float a1, float a2, float a3) {
+    float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+    asm("v_mul_f32_e32 %0, %4, %0\n\tv_mul_f32_e32 %1, %5, %1\n\tv_mul_f32_e32 %2, %6, %2\n\tv_mul_f32_e32 %3, %7, %3"
+        : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
+        : "v"(a0), "v"(a1), "v"(a2), "v"(a3));
+    x = floatx4{x0, x1, x2, x3};
+}
+__device__ __forceinline__ float half_at(uint32_t w, int hi) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(hi ? (w >> 16) : (w & 0xFFFFu)));
+}
+
+// K-code table indexed by one packed byte (low nibble = even dim, high nibble = odd dim):
+// entry e = ((c_hi[lo], c_hi[hi]), (c_lo[lo], c_lo[hi])) as two f16 pairs, read with one
+// ds_read_b64 straight into half of a QK^T operand; AoS adds a second table of
+// c[lo]^2 + c[hi]^2 (fp32) for the norm correction.
+template <int LAYOUT> struct KTable {
+    static constexpr int words = LAYOUT == 0 ? 512 : 768;
+};
+
+template <int LAYOUT>
+__device__ __forceinline__ void build_key_table(uint32_t *tbl, const float *pair_lut, int lane) {
+    for (int e = lane; e < 256; e += kWave) {
+        const int lo = e & 15, hi = e >> 4;
+        const float c_lo = pair_lut[2 * (lo * 16 + hi)];  // row (lo, hi) = (c[lo], c[hi])
+        const float c_hi = pair_lut[2 * (lo * 16 + hi) + 1];
+        const uint32_t p_lo = split_f16(c_lo), p_hi = split_f16(c_hi);
+        tbl[2 * e] = (p_lo & 0xFFFFu) | (p_hi << 16);
+        tbl[2 * e + 1] = (p_lo >> 16) | (p_hi & 0xFFFF0000u);
+        if constexpr (LAYOUT == 1)
+            tbl[512 + e] = fbits(c_lo * c_lo + c_hi * c_hi);
+    }
+}
+
+// Per-lane byte offsets inside a KV block (fixed for a kernel instance); steps that are
+// the same for every lane travel in the loads' scalar offsets.
+struct LaneOffsets {
+    uint32_t k;      // K bytes loaded by the lane: token 4g + n / 4, bytes 16 (n % 4) ..
+    int kperm;       // 4 x the lane that loads the K bytes this lane needs (token n, bytes 16g ..)
+    uint32_t v0;     // V dword n of token 4g; token 4g+i adds i * tok_stride
+    uint32_t m;      // SoA: norm of the lane's first softmax token within its field array; AoS: its slot
+    int tok_stride;  // bytes between consecutive tokens of one kv-head
+    int mf;          // SoA: bytes between the three metadata arrays
+    int v_shift;     // AoS: v0 & 3 (the same in every lane)
+};
+
+template <int LAYOUT, int G>
+__device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int hk, int block_size) {
+    constexpr int TPL = G / 4;
+    const int st = 4 * g + TPL * (n / G);  // first softmax token of the lane
+    const int rec = LAYOUT == 0 ? kSoaRecord : kAosSlot;
+    LaneOffsets o;
+    o.tok_stride = hk * rec;
+    // K is loaded coalesced (each 16-lane row reads 4 whole 64-byte K records) and then
+    // permuted across lanes into the MFMA layout (lane (n, g) = token n, bytes 16g ..).
+    o.k = ((4 * g + (n >> 2)) * hk + kvh) * rec + 16 * (n & 3);
+    o.kperm = 4 * (16 * (n >> 2) + 4 * (n & 3) + g);
+    o.v0 = (4 * g * hk + kvh) * rec + kHalfD + (LAYOUT == 0 ? 0 : 2) + 4 * n;
+    if (LAYOUT == 0) {
+        o.m = (kvh * 3 * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
+        o.mf = block_size * 2;
+        o.v_shift = 0;
+    } else {
+        o.m = (st * hk + kvh) * kAosSlot;
+        o.mf = 0;
+        o.v_shift = (kvh * kAosSlot + kHalfD + 2) & 3;  // lane terms are multiples of 4
+    }
+    return o;
+}
+
+// Raw K loads of one tile.
+template <int LAYOUT> struct RawK;
+template <> struct RawK<0> { uint4 k; };
+template <> struct RawK<1> { uint32_t k[5]; };  // aligned dwords around the 2-byte aligned bytes
+// Raw V + metadata loads of one tile.  SoA metadata of two consecutive tokens comes in
+// one dword (TPL = 2); AoS metadata in one 16-bit load per token and field.
+template <int LAYOUT, int TPL> struct RawV;
+template <int TPL> struct RawV<0, TPL> {
+    uint32_t v[4];
+    uint32_t norm, scale, zero;
+};
+template <int TPL> struct RawV<1, TPL> {
+    uint2 v[4];  // aligned dword pairs around each V dword
+    uint32_t norm[TPL], scale[TPL], zero[TPL];
+};
+
+template <int LAYOUT>
+__device__ __forceinline__ void issue_k(RawK<LAYOUT> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
+                                        const LaneOffsets &o) {
+    if constexpr (LAYOUT == 0) {
+        t.k = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
+    } else {
+        const uint32_t ka = o.k & ~3u;
+        const auto k03 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ka, doff, 0);
+        t.k[0] = k03[0];
+        t.k[1] = k03[1];
+        t.k[2] = k03[2];
+        t.k[3] = k03[3];
+        t.k[4] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, ka + 16, doff, 0);
+    }
+}
+
+template <int LAYOUT, int TPL>
+__device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
+                                        int moff, const LaneOffsets &o) {
+    if constexpr (LAYOUT == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
+        if constexpr (TPL == 1) {
+            t.norm = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff, 0);
+            t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff + o.mf, 0);
+            t.zero = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff + 2 * o.mf, 0);
+        } else {
+            t.norm = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m, moff, 0);
+            t.scale = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m, moff + o.mf, 0);
+            t.zero = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m, moff + 2 * o.mf, 0);
+        }
+    } else {
+        // token 4g+i's V dword starts sh = (v_shift + i * tok_stride) & 3 bytes past a
+        // dword; both offsets below are multiples of 4 and non-negative.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int sh = (o.v_shift + i * o.tok_stride) & 3;
+            t.v[i] = __builtin_bit_cast(
+                uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                           rsrc, o.v0 - o.v_shift, doff + i * o.tok_stride + o.v_shift - sh, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < TPL; ++j) {
+            t.norm[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHalfD, doff + j * o.tok_stride, 0);
+            t.scale[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHeadDim + 2, doff + j * o.tok_stride, 0);
+            t.zero[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHeadDim + 4, doff + j * o.tok_stride, 0);
+        }
+    }
+}
+
+// The K bytes of lane (n, g) (token n, bytes 16g ..), gathered from the loading lanes.
+template <int LAYOUT>
+__device__ __forceinline__ uint4 decode_k(const RawK<LAYOUT> &t, const LaneOffsets &o) {
+    uint4 w;
+    if constexpr (LAYOUT == 0) {
+        w = t.k;
+    } else {
+        const uint32_t sh = o.k & 3u;
+        w = uint4{__builtin_amdgcn_alignbyte(t.k[1], t.k[0], sh), __builtin_amdgcn_alignbyte(t.k[2], t.k[1], sh),
+                  __builtin_amdgcn_alignbyte(t.k[3], t.k[2], sh), __builtin_amdgcn_alignbyte(t.k[4], t.k[3], sh)};
+    }
+    return uint4{(uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.x),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.y),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.z),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.w)};
+}
+
+// V dwords and metadata of one tile; metadata as f16 pairs (token j in half j).
+struct TileV {
+    uint32_t v[4];
+    uint32_t norm, scale, zero;
+};
+
+template <int LAYOUT, int TPL>
+__device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const LaneOffsets &o) {
+    TileV r;
+    if constexpr (LAYOUT == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            r.v[i] = t.v[i];
+        r.norm = t.norm;
+        r.scale = t.scale;
+        r.zero = t.zero;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            r.v[i] = __builtin_amdgcn_alignbyte(t.v[i].y, t.v[i].x, (o.v_shift + i * o.tok_stride) & 3);
+        if constexpr (TPL == 1) {
+            r.norm = t.norm[0];
+            r.scale = t.scale[0];
+            r.zero = t.zero[0];
+        } else {
+            r.norm = (t.norm[0] & 0xFFFFu) | (t.norm[1] << 16);
+            r.scale = (t.scale[0] & 0xFFFFu) | (t.scale[1] << 16);
+            r.zero = (t.zero[0] & 0xFFFFu) | (t.zero[1] << 16);
+        }
+    }
+    return r;
+}
+
+// Running softmax state of a lane: the shared max of its head (as -m, exp2 domain;
+// +FLT_MAX = "no token yet"), the lane's own partial sums.
+struct State {
+    float negm, l, z;
+};
+
+// Lane constants of the token selection / operand packing.
+struct LaneConst {
+    int n, g;
+    bool tok_bit0, tok_bit1;  // G = 4: register index n / 4 of the lane's token
+    bool upper;               // n >= 8: rows / columns of the lo part
+    uint32_t part_sel;        // v_perm selector of the lane's part (hi / lo halves)
+};
+
+// q as B operands of the 8 QK^T MFMAs of a tile.  MFMA m covers the lane's code bytes
+// 2m, 2m+1 (dims d = 32g + 4m .. +3); its A slots are (c_hi, c_hi, c_lo, c_lo) of byte 2m
+// then of byte 2m+1, so bq[m] = (Q(2m), Q(2m), Q(2m+1), Q(2m+1)) with Q(b) the f16 pair
+// q_part(n)[head kvh*G + (n & (G-1))][32g + 2b, 32g + 2b + 1].
+template <int G>
+__device__ __forceinline__ void load_q(half8 (&bq)[8], const float *__restrict__ q_rot, int64_t head_row,
+                                       int n, int g, float scale) {
+    const float *qp = q_rot + head_row * kHeadDim + 32 * g;
+    const bool lo = n >= 8;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const float4 x = *reinterpret_cast<const float4 *>(qp + 4 * m);
+        const uint32_t s0 = split_f16(x.x * scale), s1 = split_f16(x.y * scale);
+        const uint32_t s2 = split_f16(x.z * scale), s3 = split_f16(x.w * scale);
+        const uint32_t w0 = lo ? ((s0 >> 16) | (s1 & 0xFFFF0000u)) : ((s0 & 0xFFFFu) | (s1 << 16));
+        const uint32_t w1 = lo ? ((s2 >> 16) | (s3 & 0xFFFF0000u)) : ((s2 & 0xFFFFu) | (s3 << 16));
+        bq[m] = as_half8(w0, w0, w1, w1);
+    }
+}
+
+// K-table entries of one tile's 16 code bytes (dims 32g + 2b, 32g + 2b + 1 for byte b),
+// read from LDS at the top of a stage so that their latency is covered by the softmax
+// that runs meanwhile; AoS also sums the lane's share of ||c[idx]||^2.
+struct KOps {
+    uint2 e[16];
+    float csq;
+};
+
+template <int LAYOUT>
+__device__ __forceinline__ KOps lookup_tile(const uint4 &k, const uint32_t *ktab) {
+    KOps r;
+    const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
+    const uint2 *t2 = reinterpret_cast<const uint2 *>(ktab);
+#pragma unroll
+    for (int b = 0; b < 16; ++b)
+        r.e[b] = t2[(kw[b >> 2] >> (8 * (b & 3))) & 0xFFu];
+    r.csq = 0.f;
+    if constexpr (LAYOUT == 1) {
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+            r.csq += bitsf(ktab[512 + ((kw[b >> 2] >> (8 * (b & 3))) & 0xFFu)]);
+    }
+    return r;
+}
+
+__device__ __forceinline__ half8 k_operand(const KOps &k, int m) {
+    return as_half8(k.e[2 * m].x, k.e[2 * m].y, k.e[2 * m + 1].x, k.e[2 * m + 1].y);
+}
+
+// QK^T of one tile from its looked-up entries: 8 MFMAs in two accumulation chains.
+__device__ __forceinline__ floatx4 qk_tile(const KOps &k, const half8 (&bq)[8]) {
+    floatx4 h = {0.f, 0.f, 0.f, 0.f}, l = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; m += 2) {
+        h = mfma(k_operand(k, m), bq[m], h);
+        l = mfma(k_operand(k, m + 1), bq[m + 1], l);
+    }
+    return h + l;
+}
+
+// PV of a pair of tiles (A operand aw, V dwords va / vb of tokens 4g .. 4g+3) interleaved
+// with QK^T of the next tile.  Accumulator 2m takes the even dim's codes (low nibbles),
+// accumulator 2m + 1 the whole bytes (lo + 16 * hi); the odd dim is recovered as
+// (acc[2m+1] - acc[2m]) / 16 when the split's rows are written.
+__device__ __forceinline__ floatx4 pv_qk(floatx4 (&acc)[8], const uint32_t (&aw)[4], const uint32_t (&va)[4],
+                                         const uint32_t (&vb)[4], const KOps &k, const half8 (&bq)[8]) {
+    const half8 a = as_half8(aw[0], aw[1], aw[2], aw[3]);
+    floatx4 h = {0.f, 0.f, 0.f, 0.f}, l = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        // byte m (dims 8n + 2m, 8n + 2m + 1) of two tokens' dwords -> (byte, 0, byte, 0)
+        const uint32_t sel = (uint32_t)m | 0x0C00u | ((uint32_t)(4 + m) << 16) | 0x0C000000u;
+        const uint32_t p0 = __builtin_amdgcn_perm(va[1], va[0], sel), p1 = __builtin_amdgcn_perm(va[3], va[2], sel);
+        const uint32_t p2 = __builtin_amdgcn_perm(vb[1], vb[0], sel), p3 = __builtin_amdgcn_perm(vb[3], vb[2], sel);
+        h = mfma(k_operand(k, 2 * m), bq[2 * m], h);
+        acc[2 * m] = mfma(a, as_half8(p0 & 0x000F000Fu, p1 & 0x000F000Fu, p2 & 0x000F000Fu, p3 & 0x000F000Fu),
+                          acc[2 * m]);
+        l = mfma(k_operand(k, 2 * m + 1), bq[2 * m + 1], l);
+        acc[2 * m + 1] = mfma(a, as_half8(p0, p1, p2, p3), acc[2 * m + 1]);
+    }
+    return h + l;
+}
+
+// Full dot of the lane's TPL softmax tokens from the QK^T accumulator (+ column n ^ 8).
+template <int G>
+__device__ __forceinline__ void lane_dots(const floatx4 &acc, const LaneConst &lc, float (&dot)[G / 4]) {
+    float d[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        d[i] = acc[i] + dppf<kRor8>(acc[i]);
+    if constexpr (G == 4) {
+        const float lo = lc.tok_bit0 ? d[1] : d[0];
+        const float hi = lc.tok_bit0 ? d[3] : d[2];
+        dot[0] = lc.tok_bit1 ? hi : lo;
+    } else {
+        dot[0] = lc.upper ? d[2] : d[0];
+        dot[1] = lc.upper ? d[3] : d[1];
+    }
+}
+
+// Max over the lanes of one head (G = 4: lanes n = h mod 4 of all rows; G = 8: n = h mod 8).
+template <int G> __device__ __forceinline__ float head_max(float x) {
+    x = fmaxf(x, dppf<kRor8>(x));
+    if constexpr (G == 4)
+        x = fmaxf(x, dppf<kRor4>(x));
+    return max_xor16(max_xor32(x));
+}
+template <int G> __device__ __forceinline__ float head_sum(float x) {
+    x += dppf<kRor8>(x);
+    if constexpr (G == 4)
+        x += dppf<kRor4>(x);
+    return sum_xor16(sum_xor32(x));
+}
+
+// w * a of a pending PV A-operand dword (two tokens' w as f16 parts of the lane's row;
+// the other part sits in lane n ^ 8 of the same row), split again into the lane's part.
+__device__ __forceinline__ uint32_t rescale_pending(uint32_t d, float a, bool upper) {
+    const uint32_t other = dpp<kRor8>(d);
+    const uint32_t hi = upper ? other : d, lo = upper ? d : other;
+    const uint32_t s0 = split_f16((half_at(hi, 0) + half_at(lo, 0)) * a);
+    const uint32_t s1 = split_f16((half_at(hi, 1) + half_at(lo, 1)) * a);
+    return upper ? ((s0 >> 16) | (s1 & 0xFFFF0000u)) : ((s0 & 0xFFFFu) | (s1 << 16));
+}
+
+// Softmax of one tile -> the lane's two A-operand dwords d0 / d1 of the PV (tokens 4g ..
+// 4g+3 of the lane's head row, in its part).  dots: the lane's token dots; norm_f:
+// per-token score factors; valid: token inside the split (only boundary tiles have
+// invalid ones).  For the second tile of a pair (SECOND) the first tile's dwords p0 / p1
+// are still waiting for their PV: a max change rescales them with the accumulators.
+template <int G, bool SECOND>
+__device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const float (&norm_f)[G / 4],
+                                             const TileV &t, State &st, floatx4 (&acc)[8],
+                                             const LaneConst &lc, bool boundary,
+                                             const bool (&valid)[G / 4], uint32_t &p0, uint32_t &p1,
+                                             uint32_t &d0, uint32_t &d1) {
+    constexpr int TPL = G / 4;
+    float s2[TPL];
+    bool need = false;
+#pragma unroll
+    for (int j = 0; j < TPL; ++j)
+        s2[j] = fmaf(dot[j], norm_f[j], st.negm);  // score - m
+    if (__builtin_expect(boundary, 0)) {
+#pragma unroll
+        for (int j = 0; j < TPL; ++j)
+            s2[j] = valid[j] ? s2[j] : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < TPL; ++j)
+        need |= s2[j] > kRescaleLogX;
+    if (__builtin_expect(__any(need), 0)) {
+        // new head max from the exact scores (s2 is inexact while -m = FLT_MAX)
+        float sn[TPL];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < TPL; ++j) {
+            sn[j] = dot[j] * norm_f[j];
+            if (boundary)
+                sn[j] = valid[j] ? sn[j] : -INFINITY;
+            mx = fmaxf(mx, sn[j]);
+        }
+        mx = head_max<G>(mx);
+        const float negm_new = (mx + st.negm > kRescaleLogX) ? -mx : st.negm;
+        // exp2(m_old - m_new): 1 for heads that keep their max, 0 after a split start
+        const float alpha = __builtin_amdgcn_exp2f(negm_new - st.negm);
+        float ah[4];
+        if constexpr (G == 4) {
+            ah[0] = quad_bcast<0>(alpha);  // lane 4q + r holds head r
+            ah[1] = quad_bcast<1>(alpha);
+            ah[2] = quad_bcast<2>(alpha);
+            ah[3] = quad_bcast<3>(alpha);
+        } else {
+            // accumulator register r of lane group g = head r + 4 (g & 1); row 0 lane h
+            // holds head h
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                ah[r] = __shfl(alpha, r + 4 * (lc.g & 1), kWave);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            scale_in_place(acc[j], ah[0], ah[1], ah[2], ah[3]);
+        st.l *= alpha;
+        st.z *= alpha;
+        if constexpr (SECOND) {
+            p0 = rescale_pending(p0, alpha, lc.upper);
+            p1 = rescale_pending(p1, alpha, lc.upper);
+        }
+        st.negm = negm_new;
+#pragma unroll
+        for (int j = 0; j < TPL; ++j)
+            s2[j] = sn[j] + negm_new;
+    }
+    uint32_t y[TPL];
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) {
+        const float p = __builtin_amdgcn_exp2f(s2[j]);
+        st.l += p;
+        st.z = fmaf(p, half_at(t.zero, j), st.z);
+        y[j] = split_f16(p * half_at(t.scale, j));
+    }
+    uint32_t P, Q;
+    if constexpr (G == 4) {
+        // lane n owns token n / 4; lanes n + 4, n + 8, n + 12 own the next ones (mod 4)
+        const uint32_t x1 = dpp<kRor12>(y[0]), x2 = dpp<kRor8>(y[0]), x3 = dpp<kRor4>(y[0]);
+        P = __builtin_amdgcn_perm(x1, y[0], lc.part_sel);
+        Q = __builtin_amdgcn_perm(x3, x2, lc.part_sel);
+    } else {
+        // lane n owns tokens 2 (n / 8) + {0, 1}; lane n ^ 8 owns the other two
+        const uint32_t z0 = dpp<kRor8>(y[0]), z1 = dpp<kRor8>(y[1]);
+        P = __builtin_amdgcn_perm(y[1], y[0], lc.part_sel);
+        Q = __builtin_amdgcn_perm(z1, z0, lc.part_sel);
+    }
+    // rows 0..7 own tokens (0, 1) in P; rows 8..15 own tokens (2, 3) in P
+    d0 = lc.upper ? Q : P;
+    d1 = lc.upper ? P : Q;
+}
+
+// Write the rows of one split: lane group g ends with heads hA, hA + 1 (see rs_xor32),
+// dims 8n .. 8n + 7; lanes 0 .. G-1 write the LSE of head n.
+template <int G>
+__device__ __forceinline__ void write_split(const State &st, const floatx4 (&acc)[8], float *__restrict__ mid_o,
+                                            int64_t row0, int num_splits, int sid, const LaneConst &lc) {
+    const float lt = head_sum<G>(st.l);
+    const float zt = head_sum<G>(st.z);
+    const float safe_l = lt > 0.f ? lt : 1.f;
+    const int hA = 2 * (lc.g >> 1) + (G == 8 ? 4 * (lc.g & 1) : 0);
+    // every row holds the totals of head h in its lanes n = h (mod G)
+    const float inv_a = __builtin_amdgcn_rcpf(__shfl(safe_l, hA, kWave));
+    const float inv_b = __builtin_amdgcn_rcpf(__shfl(safe_l, hA + 1, kWave));
+    const float z_a = __shfl(zt, hA, kWave), z_b = __shfl(zt, hA + 1, kWave);
+    float oa[8], ob[8];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        // V codes entered as n * 2^-24; accumulator 2m + 1 holds (even + 16 * odd)
+        const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
+        const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
+        oa[2 * m] = fmaf(xa, 16777216.0f, z_a) * inv_a;
+        ob[2 * m] = fmaf(xb, 16777216.0f, z_b) * inv_b;
+        oa[2 * m + 1] = fmaf(ya - xa, 1048576.0f, z_a) * inv_a;
+        ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
+    }
+    if (G == 8 || (lc.g & 1) == 0) {
+        float *ra = mid_o + ((row0 + hA) * num_splits + sid) * (kHeadDim + 1) + 8 * lc.n;
+        float *rb = ra + (int64_t)num_splits * (kHeadDim + 1);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            ra[j] = oa[j];
+            rb[j] = ob[j];
+        }
+    }
+    if (lc.g == 0 && lc.n < G) {
+        float *lrow = mid_o + ((row0 + lc.n) * num_splits + sid) * (kHeadDim + 1);
+        lrow[kHeadDim] = -st.negm * kLn2 + logf(safe_l);
+    }
+}
+
+// One wave handles a run of consecutive live splits of one (sequence, kv-head).  Their
+// tiles form one stream: split s contributes n_s tiles padded to a multiple of 4 stream
+// positions (padding positions re-read the split's last tile and mask every token), so
+// split ends fall on 4-stage boundaries (after an odd stage's PV).  After a split's last
+// stage the wave writes its rows and restarts the softmax state (the first rescale of
+// the next split multiplies the old accumulators by 0).
+template <int LAYOUT, int G, int WPE>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
+    const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
+    const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
+    const float *__restrict__ pair_lut, float *__restrict__ mid_o, int num_q_heads,
+    int num_kv_heads, int block_size_log2, int max_blocks, int64_t block_stride, int num_splits,
+    float score_scale_log2) {
+    static_assert(G == 4 || G == 8, "GQA group 4 or 8");
+    constexpr int TPL = G / 4;
+    constexpr int RING = 4;
+    const int block_size = 1 << block_size_log2;
+    const int kvh = blockIdx.x;
+    const int wid = blockIdx.y, nw = gridDim.y;
+    const int b = blockIdx.z;
+    const int lane = threadIdx.x;
+    const int seq_len = seq_lens[b];
+    // split partition: L = ceil(len / S); live splits are those with s * L < len
+    const int split_len = (seq_len + num_splits - 1) / num_splits;
+    // wave x of the W waves of this (sequence, kv-head) takes splits [x * S / W, (x + 1) * S / W)
+    const int s_lo = (int)((int64_t)wid * num_splits / nw);
+    const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
+    const int s_hi = min((int)((int64_t)(wid + 1) * num_splits / nw), live);
+    if (s_lo >= s_hi)
+        return;
+
+    LaneConst lc;
+    lc.n = lane & 15;
+    lc.g = lane >> 4;
+    lc.tok_bit0 = (lc.n >> 2) & 1;
+    lc.tok_bit1 = (lc.n >> 3) & 1;
+    lc.upper = lc.n >= 8;
+    lc.part_sel = lc.upper ? 0x07060302u : 0x05040100u;
+
+    __shared__ uint32_t ktab[KTable<LAYOUT>::words];
+    build_key_table<LAYOUT>(ktab, pair_lut, lane);
+
+    half8 bq[8];
+    load_q<G>(bq, q_rot, (int64_t)b * num_q_heads + kvh * G + (lc.n & (G - 1)), lc.n, lc.g, score_scale_log2);
+
+    State st{__FLT_MAX__, 0.f, 0.f};
+    floatx4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // stream positions of a split with n tiles: n rounded up to a whole ring turn
+    auto ring_padded = [](int n) { return (n + RING - 1) & ~(RING - 1); };
+    int total = 0;
+    for (int s = s_lo; s < s_hi; ++s) {
+        const int st0 = s * split_len, en = min(st0 + split_len, seq_len);
+        total += ring_padded(((en - 1) >> 4) - (st0 >> 4) + 1);
+    }
+
+    const LaneOffsets off = lane_offsets<LAYOUT, G>(lc.n, lc.g, kvh, num_kv_heads, block_size);
+    const int32_t *bt = block_table + (int64_t)b * max_blocks;
+    const int tok0 = 4 * lc.g + TPL * (lc.n / G);  // the lane's first softmax token
+    const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
+    const int rec = LAYOUT == 0 ? kSoaRecord : kAosSlot;
+    __syncthreads();
+
+    int cur = s_lo;
+    int cur_start = cur * split_len;
+    int cur_end = min(cur_start + split_len, seq_len);
+    int cur_stop = ring_padded(((cur_end - 1) >> 4) - (cur_start >> 4) + 1);
+
+    // Lane i of base_lo / base_hi holds the address of the 16-token piece at stream
+    // position j0 + i of the current chunk (its KV block plus the piece's offset), lane i
+    // of moff_lane the SoA metadata offset relative to that address.
+    auto rsrc_at = [&](uint32_t base_lo, uint32_t base_hi, int j) {
+        const uint64_t a = ((uint64_t)__builtin_amdgcn_readlane(base_hi, j & 63) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane(base_lo, j & 63);
+        return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(a), 0, 0x7FFFFFFF, 0x00020000);
+    };
+    // The scheduling barriers keep the loads in program order, which is what lets each
+    // wait count only the loads of later tiles.
+    auto issue_kpos = [&](RawK<LAYOUT> &r, uint32_t base_lo, uint32_t base_hi, int j) {
+        const auto rsrc = rsrc_at(base_lo, base_hi, j);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_k<LAYOUT>(r, rsrc, 0, off);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto issue_vpos = [&](RawV<LAYOUT, TPL> &r, uint32_t base_lo, uint32_t base_hi, int moff_lane, int j) {
+        const auto rsrc = rsrc_at(base_lo, base_hi, j);
+        const int moff = LAYOUT == 0 ? __builtin_amdgcn_readlane(moff_lane, j & 63) : 0;
+        __builtin_amdgcn_sched_barrier(0);
+        issue_v<LAYOUT, TPL>(r, rsrc, 0, moff, off);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    floatx4 sc;         // QK^T accumulator of the next tile
+    uint4 kn;           // K bytes of the next tile, in the MFMA layout
+    float csq_tot = 0;  // AoS: ||c[idx]||^2 of token n of that tile
+    uint32_t aw[4];
+
+    // Stage j: softmax of position j, then QK^T of position j + 1; odd stages also run
+    // the PV of positions (j - 1, j).
+    auto stage = [&](int k, const RawV<LAYOUT, TPL> &vprev, const RawV<LAYOUT, TPL> &vcur,
+                     const RawK<LAYOUT> &kafter, int mask_lane, int j) {
+        // K-table lookups of the next tile first: their latency runs under the softmax
+        const KOps e = lookup_tile<LAYOUT>(kn, ktab);
+        __builtin_amdgcn_sched_barrier(0);
+        const TileV t = decode_v<LAYOUT, TPL>(vcur, off);
+        const int t0 = 16 * __builtin_amdgcn_readlane(mask_lane, j & 63);
+        const bool boundary = !(t0 >= cur_start && t0 + 16 <= cur_end);
+        float dot[TPL], nf[TPL];
+        bool valid[TPL];
+        lane_dots<G>(sc, lc, dot);
+#pragma unroll
+        for (int q = 0; q < TPL; ++q) {
+            valid[q] = (uint32_t)(t0 + tok0 + q - cur_start) < (uint32_t)(cur_end - cur_start);
+            if constexpr (LAYOUT == 0) {
+                nf[q] = half_at(t.norm, q);
+            } else {
+                // ||c[idx]||^2 of token tok0 + q: totals sit in lanes n = token (any row)
+                nf[q] = half_at(t.norm, q) * __builtin_amdgcn_rsqf(__shfl(csq_tot, tok0 + q, kWave) + 1e-16f);
+            }
+        }
+        if (k & 1)
+            softmax_tile<G, true>(dot, nf, t, st, acc, lc, boundary, valid, aw[0], aw[1], aw[2], aw[3]);
+        else
+            softmax_tile<G, false>(dot, nf, t, st, acc, lc, boundary, valid, aw[0], aw[1], aw[0], aw[1]);
+        if (k & 1) {
+            const TileV ta = decode_v<LAYOUT, TPL>(vprev, off);
+            sc = pv_qk(acc, aw, ta.v, t.v, e, bq);
+        } else {
+            sc = qk_tile(e, bq);
+        }
+        if constexpr (LAYOUT == 1)
+            csq_tot = sum_xor16(sum_xor32(e.csq));
+        // K bytes of position j + 2 into the MFMA layout (its load was issued 3 stages ago)
+        kn = decode_k<LAYOUT>(kafter, off);
+    };
+
+    // Stream positions in chunks of 64 (one block-table entry per lane).  K loads of
+    // position j + 5 are issued right after QK^T of j + 1 consumed its slot; V loads of
+    // positions j + 3, j + 4 after the PV of (j - 1, j).  Every load and stage is
+    // unconditional -- past the chunk's end a load re-reads its last tile (an L2 hit) --
+    // so all paths issue the same loads in the same order.
+    int pos_base = 0;  // stream position where split `cur` starts
+    for (int j0 = 0; j0 < total; j0 += 64) {
+        const int nchunk = min(64, total - j0);
+        const int last = j0 + nchunk - 1;
+        int tile_lane = 0, mask_lane = 0;
+        {
+            const int p = j0 + min(lane, nchunk - 1);
+            int base = 0;
+            for (int s = s_lo; s < s_hi; ++s) {
+                const int st0 = s * split_len, en = min(st0 + split_len, seq_len);
+                const int tf = st0 >> 4, nt = ((en - 1) >> 4) - tf + 1;
+                if (p >= base) {
+                    const int o = p - base;
+                    tile_lane = tf + min(o, nt - 1);
+                    mask_lane = o < nt ? tile_lane : -(1 << 24);  // padding: no valid token
+                }
+                base += ring_padded(nt);
+            }
+        }
+        uint32_t base_lo, base_hi;
+        int moff_lane;
+        {
+            const int blk = bt[(16 * tile_lane) >> block_size_log2];
+            const int toff = (16 * tile_lane) & (block_size - 1);
+            const uint64_t a = reinterpret_cast<uint64_t>(cache) + (uint64_t)((int64_t)blk * block_stride) +
+                               (uint64_t)(toff * num_kv_heads * rec);
+            base_lo = (uint32_t)a;
+            base_hi = (uint32_t)(a >> 32);
+            moff_lane = (block_size - toff) * num_kv_heads * kSoaRecord + toff * 2;
+        }
+        RawK<LAYOUT> kr[RING];
+        RawV<LAYOUT, TPL> vr[RING];
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+            issue_kpos(kr[k], base_lo, base_hi, min(j0 + k, last));
+            issue_vpos(vr[k], base_lo, base_hi, moff_lane, min(j0 + k, last));
+        }
+        {
+            const KOps e = lookup_tile<LAYOUT>(decode_k<LAYOUT>(kr[0], off), ktab);
+            sc = qk_tile(e, bq);
+            if constexpr (LAYOUT == 1)
+                csq_tot = sum_xor16(sum_xor32(e.csq));
+            kn = decode_k<LAYOUT>(kr[1], off);
+        }
+        issue_kpos(kr[0], base_lo, base_hi, min(j0 + RING, last));
+        int j = j0;
+        while (true) {
+            const int stop = min(pos_base + cur_stop, last + 1);
+            do {
+#pragma unroll
+                for (int k = 0; k < RING; ++k) {
+                    stage(k, vr[(k + RING - 1) % RING], vr[k], kr[(k + 2) % RING], mask_lane, j + k);
+                    issue_kpos(kr[(k + 1) % RING], base_lo, base_hi, min(j + k + 1 + RING, last));
+                    if (k & 1) {
+                        issue_vpos(vr[k - 1], base_lo, base_hi, moff_lane, min(j + k - 1 + RING, last));
+                        issue_vpos(vr[k], base_lo, base_hi, moff_lane, min(j + k + RING, last));
+                    }
+                }
+                j += RING;
+            } while (j < stop);
+            if (j == pos_base + cur_stop) {
+                write_split<G>(st, acc, mid_o, row0, num_splits, cur, lc);
+                st.negm = __FLT_MAX__;
+                pos_base = j;
+                ++cur;
+                cur_start = cur * split_len;
+                cur_end = min(cur_start + split_len, seq_len);
+                cur_stop = ring_padded(((cur_end - 1) >> 4) - (cur_start >> 4) + 1);
+            }
+            if (j > last)
+                break;
+        }
+    }
+}
+
+}  // namespace xdl
+}  // namespace tq4

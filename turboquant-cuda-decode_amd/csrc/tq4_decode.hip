@@ -14,6 +14,7 @@
 #include "../../include/tq4_decode.h"
 #include "stage1_mfma.h"
 #include "stage1_simple.h"
+#include "stage1_xdl.h"
 #include "stage2.h"
 
 namespace {
@@ -102,21 +103,18 @@ template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t
 #endif
 constexpr int kStage1Ring = TQ4_STAGE1_RING;  // tiles in flight per wave
 
-template <int LAYOUT, int NSET> int waves_per_sequence(const Stage1Args &a) {
+int waves_per_sequence(const Stage1Args &a, const void *kernel, int &slots) {
     static const int forced = [] {
         const char *e = getenv("TQ4_STAGE1_WAVES");
         return e ? atoi(e) : 0;
     }();
     if (forced > 0)
         return forced < a.S ? forced : a.S;
-    static int slots = 0;  // waves the device holds at once for this kernel
-    if (!slots) {
+    if (!slots) {  // waves the device holds at once for this kernel
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, reinterpret_cast<const void *>(&tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>),
-                tq4::kWave, 0) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, tq4::kWave, 0) == hipSuccess &&
             cus > 0 && per_cu > 0)
             slots = cus * per_cu;
         else
@@ -132,10 +130,25 @@ template <int LAYOUT, int NSET> int waves_per_sequence(const Stage1Args &a) {
 }
 
 template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_t st) {
-    const dim3 grid(a.Hk, waves_per_sequence<LAYOUT, NSET>(a), a.B);
+    static int slots = 0;
+    const dim3 grid(a.Hk,
+                    waves_per_sequence(a, reinterpret_cast<const void *>(
+                                              &tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>),
+                                       slots),
+                    a.B);
     hipLaunchKernelGGL((tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>), grid, dim3(tq4::kWave), 0, st,
                        a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk,
                        log2_int(a.bs), a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
+}
+
+// The 16x16x32 kernel is compiled for 2 waves per SIMD (its register budget: 256 VGPRs).
+template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
+    static int slots = 0;
+    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, 2>;
+    const dim3 grid(a.Hk, waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots), a.B);
+    hipLaunchKernelGGL(kernel, grid, dim3(tq4::kWave), 0, st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
+                       a.mid_o, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks, a.stride, a.S,
+                       a.scale * tq4::kLog2e);
 }
 
 template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
@@ -169,16 +182,32 @@ template <int LAYOUT> int dispatch_mfma(const Stage1Args &a, hipStream_t st) {
     return launch_status("stage1_mfma");
 }
 
+template <int LAYOUT> int dispatch_xdl(const Stage1Args &a, hipStream_t st) {
+    if (!mfma_applies(a))
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: XDL kernel needs GQA group 4 or 8, a "
+                                       "power-of-two block_size >= 16 and a 16-byte block stride");
+    if (a.Hq / a.Hk == 4)
+        launch_xdl<LAYOUT, 4>(a, st);
+    else
+        launch_xdl<LAYOUT, 8>(a, st);
+    return launch_status("stage1_xdl");
+}
+
 int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     int rc = check_stage1(a);
     if (rc)
         return rc;
+    // AUTO: the 16x16x32 kernel for SoA caches, the 4x4x4 kernel for AoS (whose unaligned
+    // 134-byte slots need more registers than the 16x16x32 kernel's budget leaves).
     if (kernel == TQ4_KERNEL_AUTO)
-        kernel = mfma_applies(a) ? TQ4_KERNEL_MFMA : TQ4_KERNEL_SIMPLE;
+        kernel = !mfma_applies(a) ? TQ4_KERNEL_SIMPLE
+                                  : (a.layout == TQ4_LAYOUT_SOA ? TQ4_KERNEL_XDL : TQ4_KERNEL_MFMA);
     if (kernel == TQ4_KERNEL_MFMA)
         return a.layout == TQ4_LAYOUT_SOA ? dispatch_mfma<0>(a, st) : dispatch_mfma<1>(a, st);
     if (kernel == TQ4_KERNEL_SIMPLE)
         return a.layout == TQ4_LAYOUT_SOA ? dispatch_simple<0>(a, st) : dispatch_simple<1>(a, st);
+    if (kernel == TQ4_KERNEL_XDL)
+        return a.layout == TQ4_LAYOUT_SOA ? dispatch_xdl<0>(a, st) : dispatch_xdl<1>(a, st);
     return fail(TQ4_E_INVALID, "tq4_stage1_ex: unknown kernel id %d", kernel);
 }
 

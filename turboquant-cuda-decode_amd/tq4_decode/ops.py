@@ -26,7 +26,7 @@ from . import _lib
 from ._lib import Tq4Error  # noqa: F401  (raised by every wrapper)
 from .layout import AOS, LAYOUTS, SOA, slot_bytes
 
-KERNELS = {"auto": 0, "simple": 1, "mfma": 2}
+KERNELS = {"auto": 0, "simple": 1, "mfma": 2, "xdl": 3}
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 HEAD_DIM = 128
 
