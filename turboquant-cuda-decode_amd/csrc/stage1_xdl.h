@@ -41,6 +41,7 @@ namespace tq4 {
 namespace xdl {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kRescaleLogX = 8.0f;
 constexpr int kRor4 = 0x124, kRor8 = 0x128, kRor12 = 0x12C;  // DPP row_ror:N
@@ -512,11 +513,22 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
     d1 = lc.upper ? P : Q;
 }
 
-// Write the rows of one split: lane group g ends with heads hA, hA + 1 (see rs_xor32),
-// dims 8n .. 8n + 7; lanes 0 .. G-1 write the LSE of head n.
+// Split rows go to mid_o through an LDS image of the wave's part of it: for head h the
+// image holds the rows of up to SpanCap<G>::splits consecutive splits back to back (129
+// floats each, as in mid_o), and one flush writes each head's run with contiguous 16-byte
+// stores.  A few long write runs instead of one 516-byte row per head and split keep the
+// HBM writes from breaking up the read stream.
+template <int G> struct SpanCap {
+    static constexpr int splits = G == 4 ? 8 : 4;                           // rows per head
+    static constexpr int head_floats = (splits * (kHeadDim + 1) + 3) & ~3;  // 16 B aligned
+    static constexpr int floats = G * head_floats;
+};
+
+// Rows of one split into image slot j: lane group g ends with heads hA, hA + 1 (see
+// rs_xor32), dims 8n .. 8n + 7; lanes 0 .. G-1 hold the LSE of head n.
 template <int G>
-__device__ __forceinline__ void write_split(const State &st, const floatx4 (&acc)[8], float *__restrict__ mid_o,
-                                            int64_t row0, int num_splits, int sid, const LaneConst &lc) {
+__device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc)[8], const LaneConst &lc,
+                                            float *img, int j) {
     const float lt = head_sum<G>(st.l);
     const float zt = head_sum<G>(st.z);
     const float safe_l = lt > 0.f ? lt : 1.f;
@@ -537,26 +549,54 @@ __device__ __forceinline__ void write_split(const State &st, const floatx4 (&acc
         ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
     }
     if (G == 8 || (lc.g & 1) == 0) {
-        float *ra = mid_o + ((row0 + hA) * num_splits + sid) * (kHeadDim + 1) + 8 * lc.n;
-        float *rb = ra + (int64_t)num_splits * (kHeadDim + 1);
+        float *ra = img + hA * SpanCap<G>::head_floats + j * (kHeadDim + 1) + 8 * lc.n;
+        float *rb = ra + SpanCap<G>::head_floats;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            ra[j] = oa[j];
-            rb[j] = ob[j];
+        for (int i = 0; i < 8; ++i) {
+            ra[i] = oa[i];
+            rb[i] = ob[i];
         }
     }
-    if (lc.g == 0 && lc.n < G) {
-        float *lrow = mid_o + ((row0 + lc.n) * num_splits + sid) * (kHeadDim + 1);
-        lrow[kHeadDim] = -st.negm * kLn2 + logf(safe_l);
+    if (lc.g == 0 && lc.n < G)
+        img[lc.n * SpanCap<G>::head_floats + j * (kHeadDim + 1) + kHeadDim] = -st.negm * kLn2 + logf(safe_l);
+}
+
+// Write image slots 0 .. ns-1 to the rows of splits s0 .. s0+ns-1.  Rows of one head and
+// consecutive splits are consecutive in mid_o [B, Hq, S, D + 1], so head h's slots are one
+// run of ns * 129 floats.  One wave: its LDS accesses complete in program order, so only
+// the compiler must keep the image reads after the writes.
+template <int G>
+__device__ __forceinline__ void flush_splits(const float *img, float *__restrict__ mid_o, int64_t row0,
+                                             int num_splits, int s0, int ns, int lane) {
+    asm volatile("" ::: "memory");
+    const int64_t head_bytes = (int64_t)num_splits * (kHeadDim + 1) * 4;
+    float *base = mid_o + (row0 * num_splits + s0) * (kHeadDim + 1);
+    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7FFFFFFF, 0x00020000);
+    const int run = ns * (kHeadDim + 1);  // floats per head
+    const int chunks = run >> 2;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float *src = img + h * SpanCap<G>::head_floats;
+        for (int c = lane; c < chunks; c += kWave) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + 4 * c);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)}, out,
+                (int)(h * head_bytes) + 16 * c, 0, 0);
+        }
+        if (lane < (run & 3))
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(src[4 * chunks + lane]), out,
+                                                  (int)(h * head_bytes) + 16 * chunks + 4 * lane, 0, 0);
     }
+    asm volatile("" ::: "memory");
 }
 
 // One wave handles a run of consecutive live splits of one (sequence, kv-head).  Their
 // tiles form one stream: split s contributes n_s tiles padded to a multiple of 4 stream
 // positions (padding positions re-read the split's last tile and mask every token), so
 // split ends fall on 4-stage boundaries (after an odd stage's PV).  After a split's last
-// stage the wave writes its rows and restarts the softmax state (the first rescale of
-// the next split multiplies the old accumulators by 0).
+// stage the wave puts its rows into the LDS image (flushed to mid_o when full and after
+// the wave's last split) and restarts the softmax state (the first rescale of the next
+// split multiplies the old accumulators by 0).
 template <int LAYOUT, int G, int WPE>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
@@ -591,6 +631,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     lc.part_sel = lc.upper ? 0x07060302u : 0x05040100u;
 
     __shared__ uint32_t ktab[KTable<LAYOUT>::words];
+    __shared__ __align__(16) float img[SpanCap<G>::floats];
     build_key_table<LAYOUT>(ktab, pair_lut, lane);
 
     half8 bq[8];
@@ -618,6 +659,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     __syncthreads();
 
     int cur = s_lo;
+    int img_s0 = s_lo;  // split of image slot 0
     int cur_start = cur * split_len;
     int cur_end = min(cur_start + split_len, seq_len);
     int cur_stop = ring_padded(((cur_end - 1) >> 4) - (cur_start >> 4) + 1);
@@ -756,7 +798,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                 j += RING;
             } while (j < stop);
             if (j == pos_base + cur_stop) {
-                write_split<G>(st, acc, mid_o, row0, num_splits, cur, lc);
+                stash_split<G>(st, acc, lc, img, cur - img_s0);
+                if (cur + 1 == s_hi || cur + 1 - img_s0 == SpanCap<G>::splits) {
+                    flush_splits<G>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
+                    img_s0 = cur + 1;
+                }
                 st.negm = __FLT_MAX__;
                 pos_base = j;
                 ++cur;
