@@ -53,12 +53,9 @@ def algorithmic_bytes(w) -> int:
 
 
 def effective_kernel(layout: str, kernel: str) -> str:
-    """The kernel a launch runs: ``auto`` picks the 16x16x32 MFMA kernel (xdl) for SoA
-    caches and the 4x4x4 MFMA kernel for AoS caches (the GQA groups and block sizes of
-    this workload are ones both support)."""
-    if kernel != "auto":
-        return kernel
-    return "xdl" if layout == "soa" else "mfma"
+    """The kernel a launch runs: ``auto`` picks the 16x16x32 MFMA kernel (xdl) for both
+    cache layouts (this workload's GQA group and block size are ones it supports)."""
+    return "xdl" if kernel == "auto" else kernel
 
 
 def traffic_from_profile(name: str):

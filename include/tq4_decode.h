@@ -65,8 +65,8 @@ int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block
 /* Same as tq4_stage1 with an explicit kernel choice (TQ4_KERNEL_*): SIMPLE is the
  * plain-VALU kernel (any GQA group up to 16); MFMA (v_mfma_f32_4x4x4_16b_f16) and XDL
  * (v_mfma_f32_16x16x32_f16) are the matrix-core kernels (GQA group 4 or 8, block_size a
- * power of two >= 16, cache_block_stride a multiple of 16).  AUTO picks XDL for SoA and
- * MFMA for AoS caches when they apply, SIMPLE otherwise.
+ * power of two >= 16, cache_block_stride a multiple of 16).  AUTO picks XDL when it
+ * applies, SIMPLE otherwise.
  * Replaces: the per-version entry points tq4_cuda_v1 .. tq4_cuda_v9 (cuda/tq4_cuda_vN_bind.cpp). */
 int tq4_stage1_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
                   const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,

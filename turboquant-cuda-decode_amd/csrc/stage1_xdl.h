@@ -95,15 +95,6 @@ __device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, ui
 __device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-// x *= a in x's own register (a tied operand), so that a rarely taken rescale does not
-// give the accumulators new registers that the common path would have to copy into.
-__device__ __forceinline__ void scale_in_place(floatx4 &x, float a0, float a1, float a2, float a3) {
-    float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
-    asm("v_mul_f32_e32 %0, %4, %0\n\tv_mul_f32_e32 %1, %5, %1\n\tv_mul_f32_e32 %2, %6, %2\n\tv_mul_f32_e32 %3, %7, %3"
-        : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
-        : "v"(a0), "v"(a1), "v"(a2), "v"(a3));
-    x = floatx4{x0, x1, x2, x3};
-}
 __device__ __forceinline__ float half_at(uint32_t w, int hi) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(hi ? (w >> 16) : (w & 0xFFFFu)));
 }
@@ -287,6 +278,7 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
 // +FLT_MAX = "no token yet"), the lane's own partial sums.
 struct State {
     float negm, l, z;
+    float pend;  // rescale of the accumulators still owed for the lane's head (applied by the next PV stage)
 };
 
 // Lane constants of the token selection / operand packing.
@@ -424,8 +416,11 @@ __device__ __forceinline__ uint32_t rescale_pending(uint32_t d, float a, bool up
 // Softmax of one tile -> the lane's two A-operand dwords d0 / d1 of the PV (tokens 4g ..
 // 4g+3 of the lane's head row, in its part).  dots: the lane's token dots; norm_f:
 // per-token score factors; valid: token inside the split (only boundary tiles have
-// invalid ones).  For the second tile of a pair (SECOND) the first tile's dwords p0 / p1
-// are still waiting for their PV: a max change rescales them with the accumulators.
+// invalid ones).  A max change on the first tile of a pair only records the factor the
+// accumulators owe (st.pend); the second tile (SECOND) applies it, with its own, before
+// the pair's PV, and rescales the first tile's dwords p0 / p1, still waiting for that PV.
+// Only the second tile's rare branch touches the accumulators, so the common path keeps
+// them in place.
 template <int G, bool SECOND>
 __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const float (&norm_f)[G / 4],
                                              const TileV &t, State &st, floatx4 (&acc)[8],
@@ -446,6 +441,8 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
 #pragma unroll
     for (int j = 0; j < TPL; ++j)
         need |= s2[j] > kRescaleLogX;
+    if constexpr (SECOND)
+        need |= st.pend != 1.f;
     if (__builtin_expect(__any(need), 0)) {
         // new head max from the exact scores (s2 is inexact while -m = FLT_MAX)
         float sn[TPL];
@@ -461,27 +458,32 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
         const float negm_new = (mx + st.negm > kRescaleLogX) ? -mx : st.negm;
         // exp2(m_old - m_new): 1 for heads that keep their max, 0 after a split start
         const float alpha = __builtin_amdgcn_exp2f(negm_new - st.negm);
-        float ah[4];
-        if constexpr (G == 4) {
-            ah[0] = quad_bcast<0>(alpha);  // lane 4q + r holds head r
-            ah[1] = quad_bcast<1>(alpha);
-            ah[2] = quad_bcast<2>(alpha);
-            ah[3] = quad_bcast<3>(alpha);
-        } else {
-            // accumulator register r of lane group g = head r + 4 (g & 1); row 0 lane h
-            // holds head h
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                ah[r] = __shfl(alpha, r + 4 * (lc.g & 1), kWave);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            scale_in_place(acc[j], ah[0], ah[1], ah[2], ah[3]);
         st.l *= alpha;
         st.z *= alpha;
         if constexpr (SECOND) {
+            const float owed = alpha * st.pend;
+            st.pend = 1.f;
+            float ah[4];
+            if constexpr (G == 4) {
+                ah[0] = quad_bcast<0>(owed);  // lane 4q + r holds head r
+                ah[1] = quad_bcast<1>(owed);
+                ah[2] = quad_bcast<2>(owed);
+                ah[3] = quad_bcast<3>(owed);
+            } else {
+                // accumulator register r of lane group g = head r + 4 (g & 1); row 0 lane h
+                // holds head h
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    ah[r] = __shfl(owed, r + 4 * (lc.g & 1), kWave);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[j] *= floatx4{ah[0], ah[1], ah[2], ah[3]};
             p0 = rescale_pending(p0, alpha, lc.upper);
             p1 = rescale_pending(p1, alpha, lc.upper);
+        } else if (st.negm != __FLT_MAX__) {
+            // (a split's first tile finds the accumulators already cleared: nothing owed)
+            st.pend *= alpha;
         }
         st.negm = negm_new;
 #pragma unroll
@@ -514,19 +516,24 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
 }
 
 // Split rows go to mid_o through an LDS image of the wave's part of it: for head h the
-// image holds the rows of up to SpanCap<G>::splits consecutive splits back to back (129
+// image holds the rows of up to Cap::splits consecutive splits back to back (129
 // floats each, as in mid_o), and one flush writes each head's run with contiguous 16-byte
 // stores.  A few long write runs instead of one 516-byte row per head and split keep the
 // HBM writes from breaking up the read stream.
-template <int G> struct SpanCap {
-    static constexpr int splits = G == 4 ? 8 : 4;                           // rows per head
-    static constexpr int head_floats = (splits * (kHeadDim + 1) + 3) & ~3;  // 16 B aligned
+// The image takes what the K-code table leaves of a wave's share of the CU's 160 KB LDS
+// at WPE waves per SIMD.
+template <int LAYOUT, int G, int WPE> struct SpanCap {
+    static constexpr int bytes = 160 * 1024 / (4 * WPE) - KTable<LAYOUT>::words * 4;
+    static constexpr int row_floats = kHeadDim + 1;
+    static constexpr int splits = (bytes / 4 / G) / row_floats;         // rows per head
+    static constexpr int head_floats = (splits * row_floats + 3) & ~3;  // 16 B aligned
     static constexpr int floats = G * head_floats;
+    static_assert(splits >= 1 && floats * 4 <= bytes, "LDS image does not fit");
 };
 
 // Rows of one split into image slot j: lane group g ends with heads hA, hA + 1 (see
 // rs_xor32), dims 8n .. 8n + 7; lanes 0 .. G-1 hold the LSE of head n.
-template <int G>
+template <int G, class Cap>
 __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc)[8], const LaneConst &lc,
                                             float *img, int j) {
     const float lt = head_sum<G>(st.l);
@@ -549,8 +556,8 @@ __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc
         ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
     }
     if (G == 8 || (lc.g & 1) == 0) {
-        float *ra = img + hA * SpanCap<G>::head_floats + j * (kHeadDim + 1) + 8 * lc.n;
-        float *rb = ra + SpanCap<G>::head_floats;
+        float *ra = img + hA * Cap::head_floats + j * (kHeadDim + 1) + 8 * lc.n;
+        float *rb = ra + Cap::head_floats;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             ra[i] = oa[i];
@@ -558,14 +565,14 @@ __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc
         }
     }
     if (lc.g == 0 && lc.n < G)
-        img[lc.n * SpanCap<G>::head_floats + j * (kHeadDim + 1) + kHeadDim] = -st.negm * kLn2 + logf(safe_l);
+        img[lc.n * Cap::head_floats + j * (kHeadDim + 1) + kHeadDim] = -st.negm * kLn2 + logf(safe_l);
 }
 
 // Write image slots 0 .. ns-1 to the rows of splits s0 .. s0+ns-1.  Rows of one head and
 // consecutive splits are consecutive in mid_o [B, Hq, S, D + 1], so head h's slots are one
 // run of ns * 129 floats.  One wave: its LDS accesses complete in program order, so only
 // the compiler must keep the image reads after the writes.
-template <int G>
+template <int G, class Cap>
 __device__ __forceinline__ void flush_splits(const float *img, float *__restrict__ mid_o, int64_t row0,
                                              int num_splits, int s0, int ns, int lane) {
     asm volatile("" ::: "memory");
@@ -576,7 +583,7 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
     const int chunks = run >> 2;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const float *src = img + h * SpanCap<G>::head_floats;
+        const float *src = img + h * Cap::head_floats;
         for (int c = lane; c < chunks; c += kWave) {
             const float4 v = *reinterpret_cast<const float4 *>(src + 4 * c);
             __builtin_amdgcn_raw_buffer_store_b128(
@@ -595,8 +602,7 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
 // positions (padding positions re-read the split's last tile and mask every token), so
 // split ends fall on 4-stage boundaries (after an odd stage's PV).  After a split's last
 // stage the wave puts its rows into the LDS image (flushed to mid_o when full and after
-// the wave's last split) and restarts the softmax state (the first rescale of the next
-// split multiplies the old accumulators by 0).
+// the wave's last split) and restarts the softmax state and the accumulators.
 template <int LAYOUT, int G, int WPE>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
@@ -631,13 +637,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     lc.part_sel = lc.upper ? 0x07060302u : 0x05040100u;
 
     __shared__ uint32_t ktab[KTable<LAYOUT>::words];
-    __shared__ __align__(16) float img[SpanCap<G>::floats];
+    using Cap = SpanCap<LAYOUT, G, WPE>;
+    __shared__ __align__(16) float img[Cap::floats];
     build_key_table<LAYOUT>(ktab, pair_lut, lane);
 
     half8 bq[8];
     load_q<G>(bq, q_rot, (int64_t)b * num_q_heads + kvh * G + (lc.n & (G - 1)), lc.n, lc.g, score_scale_log2);
 
-    State st{__FLT_MAX__, 0.f, 0.f};
+    State st{__FLT_MAX__, 0.f, 0.f, 1.f};
     floatx4 acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -798,12 +805,16 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                 j += RING;
             } while (j < stop);
             if (j == pos_base + cur_stop) {
-                stash_split<G>(st, acc, lc, img, cur - img_s0);
-                if (cur + 1 == s_hi || cur + 1 - img_s0 == SpanCap<G>::splits) {
-                    flush_splits<G>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
+                stash_split<G, Cap>(st, acc, lc, img, cur - img_s0);
+                if (cur + 1 == s_hi || cur + 1 - img_s0 == Cap::splits) {
+                    flush_splits<G, Cap>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
                     img_s0 = cur + 1;
                 }
-                st.negm = __FLT_MAX__;
+                // fresh softmax state; the next split's first max change owes nothing
+                st = State{__FLT_MAX__, 0.f, 0.f, 1.f};
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
                 pos_base = j;
                 ++cur;
                 cur_start = cur * split_len;

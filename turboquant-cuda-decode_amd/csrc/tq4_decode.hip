@@ -142,9 +142,18 @@ template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_
 }
 
 // The 16x16x32 kernel is compiled for 2 waves per SIMD (its register budget: 256 VGPRs).
+// Waves per SIMD the 16x16x32 kernel is built for.  Two: the SoA G=4 kernel also fits
+// three (168 VGPRs, a 5-split LDS image), but runs slower that way.
+#ifndef TQ4_XDL_WAVES_PER_SIMD
+#define TQ4_XDL_WAVES_PER_SIMD 2
+#endif
+template <int LAYOUT, int G> constexpr int xdl_waves_per_simd() {
+    return LAYOUT == 0 && G == 4 ? TQ4_XDL_WAVES_PER_SIMD : 2;
+}
+
 template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
     static int slots = 0;
-    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, 2>;
+    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>()>;
     const dim3 grid(a.Hk, waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots), a.B);
     hipLaunchKernelGGL(kernel, grid, dim3(tq4::kWave), 0, st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
                        a.mid_o, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks, a.stride, a.S,
@@ -197,11 +206,9 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     int rc = check_stage1(a);
     if (rc)
         return rc;
-    // AUTO: the 16x16x32 kernel for SoA caches, the 4x4x4 kernel for AoS (whose unaligned
-    // 134-byte slots need more registers than the 16x16x32 kernel's budget leaves).
+    // AUTO: the 16x16x32 kernel wherever the MFMA kernels apply (both layouts), else VALU.
     if (kernel == TQ4_KERNEL_AUTO)
-        kernel = !mfma_applies(a) ? TQ4_KERNEL_SIMPLE
-                                  : (a.layout == TQ4_LAYOUT_SOA ? TQ4_KERNEL_XDL : TQ4_KERNEL_MFMA);
+        kernel = mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE;
     if (kernel == TQ4_KERNEL_MFMA)
         return a.layout == TQ4_LAYOUT_SOA ? dispatch_mfma<0>(a, st) : dispatch_mfma<1>(a, st);
     if (kernel == TQ4_KERNEL_SIMPLE)
