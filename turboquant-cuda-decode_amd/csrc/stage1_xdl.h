@@ -22,7 +22,8 @@
 // Softmax: lane (n, g) owns TPL = G / 4 tokens: 4g + TPL * (n / G) + j, head n & (G-1).
 //   The running max m is shared by all lanes of a head and moves only when a score
 //   exceeds it by more than kRescaleLogX (p <= 2^8); that branch is rare after a
-//   split's first tile.  Each lane accumulates its own l = sum p and z = sum p * V zero.
+//   split's first tile, and only the second tile of a pair rescales the accumulators.
+//   Each lane accumulates its own l = sum p and z = sum p * V zero.
 // PV of a pair of tiles (32 tokens):  A[row][slot s] = w_part(row)[head(row)] of token
 //   4g + (s & 3) of tile s / 4, w = p * V scale (gathered from the owning lanes with DPP
 //   row rotations);  B[slot s][col n] = V code of the same token at dim 8n + j for MFMA
@@ -34,6 +35,8 @@
 // Schedule: stage t = softmax of tile t, then QK^T of tile t + 1; odd stages also run
 // the PV of tiles (t-1, t), interleaved with that QK^T.  K loads run 4 tiles ahead of
 // their QK^T, V / metadata loads 3-4 tiles ahead of their softmax.
+// Output: a finished split's rows go to an LDS image of the wave's part of mid_o, which
+// is written out as one contiguous run per head (see SpanCap).
 #pragma once
 #include "tq4_device.h"
 
