@@ -110,12 +110,27 @@ template <int LAYOUT> struct KTable {
     static constexpr int words = LAYOUT == 0 ? 512 : 768;
 };
 
+// Pair-LUT rows of the lane's table entries e = lane + 64 i (loaded before the build so
+// their latency overlaps the first KV loads).
+struct LutRows {
+    float2 r[256 / kWave];
+};
+__device__ __forceinline__ LutRows load_lut_rows(const float *pair_lut, int lane) {
+    LutRows v;
+#pragma unroll
+    for (int i = 0; i < 256 / kWave; ++i) {
+        const int e = lane + kWave * i, lo = e & 15, hi = e >> 4;
+        v.r[i] = float2{pair_lut[2 * (lo * 16 + hi)], pair_lut[2 * (lo * 16 + hi) + 1]};  // (c[lo], c[hi])
+    }
+    return v;
+}
+
 template <int LAYOUT>
-__device__ __forceinline__ void build_key_table(uint32_t *tbl, const float *pair_lut, int lane) {
-    for (int e = lane; e < 256; e += kWave) {
-        const int lo = e & 15, hi = e >> 4;
-        const float c_lo = pair_lut[2 * (lo * 16 + hi)];  // row (lo, hi) = (c[lo], c[hi])
-        const float c_hi = pair_lut[2 * (lo * 16 + hi) + 1];
+__device__ __forceinline__ void build_key_table(uint32_t *tbl, const LutRows &v, int lane) {
+#pragma unroll
+    for (int i = 0; i < 256 / kWave; ++i) {
+        const int e = lane + kWave * i;
+        const float c_lo = v.r[i].x, c_hi = v.r[i].y;
         const uint32_t p_lo = split_f16(c_lo), p_hi = split_f16(c_hi);
         tbl[2 * e] = (p_lo & 0xFFFFu) | (p_hi << 16);
         tbl[2 * e + 1] = (p_lo >> 16) | (p_hi & 0xFFFF0000u);
@@ -296,14 +311,18 @@ struct LaneConst {
 // 2m, 2m+1 (dims d = 32g + 4m .. +3); its A slots are (c_hi, c_hi, c_lo, c_lo) of byte 2m
 // then of byte 2m+1, so bq[m] = (Q(2m), Q(2m), Q(2m+1), Q(2m+1)) with Q(b) the f16 pair
 // q_part(n)[head kvh*G + (n & (G-1))][32g + 2b, 32g + 2b + 1].
-template <int G>
-__device__ __forceinline__ void load_q(half8 (&bq)[8], const float *__restrict__ q_rot, int64_t head_row,
-                                       int n, int g, float scale) {
+__device__ __forceinline__ void load_q_rows(float4 (&qx)[8], const float *__restrict__ q_rot, int64_t head_row,
+                                            int g) {
     const float *qp = q_rot + head_row * kHeadDim + 32 * g;
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+        qx[m] = *reinterpret_cast<const float4 *>(qp + 4 * m);
+}
+__device__ __forceinline__ void q_operands(half8 (&bq)[8], const float4 (&qx)[8], int n, float scale) {
     const bool lo = n >= 8;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-        const float4 x = *reinterpret_cast<const float4 *>(qp + 4 * m);
+        const float4 x = qx[m];
         const uint32_t s0 = split_f16(x.x * scale), s1 = split_f16(x.y * scale);
         const uint32_t s2 = split_f16(x.z * scale), s3 = split_f16(x.w * scale);
         const uint32_t w0 = lo ? ((s0 >> 16) | (s1 & 0xFFFF0000u)) : ((s0 & 0xFFFFu) | (s1 << 16));
@@ -621,6 +640,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const int wid = blockIdx.y, nw = gridDim.y;
     const int b = blockIdx.z;
     const int lane = threadIdx.x;
+    // The pair-LUT rows and q do not depend on the sequence length: they go out first, the
+    // K table and the q operands are built once the first tiles' loads are on their way.
+    const LutRows lut_rows = load_lut_rows(pair_lut, lane);
+    float4 q_rows[8];
+    load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + kvh * G + ((lane & 15) & (G - 1)), lane >> 4);
     const int seq_len = seq_lens[b];
     // split partition: L = ceil(len / S); live splits are those with s * L < len
     const int split_len = (seq_len + num_splits - 1) / num_splits;
@@ -642,10 +666,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     __shared__ uint32_t ktab[KTable<LAYOUT>::words];
     using Cap = SpanCap<LAYOUT, G, WPE>;
     __shared__ __align__(16) float img[Cap::floats];
-    build_key_table<LAYOUT>(ktab, pair_lut, lane);
-
     half8 bq[8];
-    load_q<G>(bq, q_rot, (int64_t)b * num_q_heads + kvh * G + (lc.n & (G - 1)), lc.n, lc.g, score_scale_log2);
 
     State st{__FLT_MAX__, 0.f, 0.f, 1.f};
     floatx4 acc[8];
@@ -666,7 +687,6 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const int tok0 = 4 * lc.g + TPL * (lc.n / G);  // the lane's first softmax token
     const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
     const int rec = LAYOUT == 0 ? kSoaRecord : kAosSlot;
-    __syncthreads();
 
     int cur = s_lo;
     int img_s0 = s_lo;  // split of image slot 0
@@ -747,14 +767,18 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     // positions j + 3, j + 4 after the PV of (j - 1, j).  Every load and stage is
     // unconditional -- past the chunk's end a load re-reads its last tile (an L2 hit) --
     // so all paths issue the same loads in the same order.
-    int pos_base = 0;  // stream position where split `cur` starts
-    for (int j0 = 0; j0 < total; j0 += 64) {
-        const int nchunk = min(64, total - j0);
-        const int last = j0 + nchunk - 1;
-        int tile_lane = 0, mask_lane = 0;
+    // chunk state: lane i holds stream position j0 + i's tile, mask and address
+    int tile_lane = 0, mask_lane = 0, moff_lane = 0;
+    uint32_t base_lo = 0, base_hi = 0;
+    RawK<LAYOUT> kr[RING];
+    RawV<LAYOUT, TPL> vr[RING];
+    // Lane tables of chunk [j0, j0 + 64) and the ring's first loads.
+    auto open_chunk = [&](int j0, int nchunk, int last) {
         {
             const int p = j0 + min(lane, nchunk - 1);
             int base = 0;
+            tile_lane = 0;
+            mask_lane = 0;
             for (int s = s_lo; s < s_hi; ++s) {
                 const int st0 = s * split_len, en = min(st0 + split_len, seq_len);
                 const int tf = st0 >> 4, nt = ((en - 1) >> 4) - tf + 1;
@@ -766,8 +790,6 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                 base += ring_padded(nt);
             }
         }
-        uint32_t base_lo, base_hi;
-        int moff_lane;
         {
             const int blk = bt[(16 * tile_lane) >> block_size_log2];
             const int toff = (16 * tile_lane) & (block_size - 1);
@@ -777,13 +799,27 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             base_hi = (uint32_t)(a >> 32);
             moff_lane = (block_size - toff) * num_kv_heads * kSoaRecord + toff * 2;
         }
-        RawK<LAYOUT> kr[RING];
-        RawV<LAYOUT, TPL> vr[RING];
 #pragma unroll
         for (int k = 0; k < RING; ++k) {
             issue_kpos(kr[k], base_lo, base_hi, min(j0 + k, last));
             issue_vpos(vr[k], base_lo, base_hi, moff_lane, min(j0 + k, last));
         }
+    };
+
+    // The first chunk's loads go out before the K table and the q operands are built.
+    open_chunk(0, min(64, total), min(64, total) - 1);
+    build_key_table<LAYOUT>(ktab, lut_rows, lane);
+    q_operands(bq, q_rows, lc.n, score_scale_log2);
+    // one wave: its LDS writes complete before its later LDS reads; only the compiler must
+    // keep the table lookups after the build
+    asm volatile("" ::: "memory");
+
+    int pos_base = 0;  // stream position where split `cur` starts
+    for (int j0 = 0; j0 < total; j0 += 64) {
+        const int nchunk = min(64, total - j0);
+        const int last = j0 + nchunk - 1;
+        if (j0 > 0)
+            open_chunk(j0, nchunk, last);
         {
             const KOps e = lookup_tile<LAYOUT>(decode_k<LAYOUT>(kr[0], off), ktab);
             sc = qk_tile(e, bq);
