@@ -75,6 +75,24 @@ def test_larger_kv_blocks(dev, kernel, bs):
         assert_parity(run(w, dev, kernel, layout, cache), oracle(w, layout, cache))
 
 
+@pytest.mark.parametrize("kernel", ["mfma", "xdl"])
+@pytest.mark.parametrize("mb,lens", [(4, [1, 60, 33]), (12, [190, 7, 160]), (13, [200, 150, 9]),
+                                     (252, [4032, 1000, 2500]), (256, [4096, 17, 3000]),
+                                     (260, [4100, 4000, 1])])
+def test_block_table_row_widths(dev, kernel, mb, lens):
+    """Block-table rows wider than a sequence needs: the entries past its need hold other
+    valid block indices, so a kernel that reads a wrong entry changes the result."""
+    w = workloads.small(105, 3, lens, 8)
+    need = w.block_table.shape[1]
+    assert need <= mb
+    nb = w.kv_cache.shape[0]
+    bt = ((np.arange(3)[:, None] * 7 + np.arange(mb)[None, :] * 3 + 1) % nb).astype(np.int32)
+    for b, n in enumerate((w.seq_lens + 15) // 16):
+        bt[b, :n] = w.block_table[b, :n]
+    w.block_table = bt
+    assert_parity(run(w, dev, kernel), oracle(w))
+
+
 def test_large_scores_rescale_path(dev):
     """q scaled x40: scores span tens of units, so the running max moves often."""
     w = workloads.small(104, 2, [640, 333], 3)
