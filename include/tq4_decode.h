@@ -108,6 +108,22 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
                     int64_t cache_block_stride, int num_kv_splits, int layout,
                     float attn_scale, tq4_stream_t stream);
 
+/*
+ * Cache writer: quantize key / value [N, Hk, D] (dtype TQ4_F32 / TQ4_BF16 / TQ4_F16,
+ * contiguous, 16-byte aligned) and write token i into cache slot slot_mapping[i]
+ * (block slot / block_size, position slot % block_size; slots < 0 are skipped).  K:
+ * norm, x_hat = k / (norm + 1e-8), y = x_hat @ rot_t (rot_t = PiT, [D, D] fp32), 4-bit
+ * index = number of the 15 midpoints <= y, stored scalar fp16(norm / ||c[idx]||) when
+ * norm_correction is nonzero (centroids [16] required), else fp16(norm).  V: 4-bit
+ * uniform codes with fp16 scale and fp16 min.  layout TQ4_LAYOUT_SOA or TQ4_LAYOUT_AOS.
+ * Replaces: triton_turboquant_store reference/soa_store.py:381-524 (MSE path, 4-bit keys
+ *           and values; kernel :223-380) and the AoS writer reference/aos_store.py.
+ */
+int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
+              const float *rot_t, const float *midpoints, const float *centroids,
+              uint8_t *kv_cache, int N, int Hk, int D, int block_size,
+              int64_t cache_block_stride, int layout, int norm_correction, tq4_stream_t stream);
+
 /* Message of the last failed call on this thread ("" when none).
  * Replaces: the TORCH_CHECK messages of cuda/tq4_cuda_v1.cu:468-499. */
 const char *tq4_last_error(void);

@@ -1,0 +1,146 @@
+"""Cache writer on the GPU (tq4_store through the C ABI) vs the oracle writer.
+
+Bar: V codes, V scale and V min are bit-exact (the same fp32 operations in the same
+order); a K index may differ from the oracle's only where y lies within float rounding
+of a midpoint (the rotation sums in a different order), and then by one bucket; the
+stored K scalar within 1 fp16 ulp; bytes of slots not written stay untouched.  Round
+trip: decoding a cache this writer filled matches the oracle's decode of the same bytes.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev
+from oracle import layout as OL
+from oracle import native
+from oracle import store as ostore
+from tq4_decode import codebook, ops, workloads
+
+pytestmark = pytest.mark.gpu
+HK, D, BS = 8, 128, 16
+TORCH = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def make_inputs(seed, n_tok, n_blocks, dtype, scale=1.0):
+    rng = np.random.default_rng(seed)
+    key = (rng.standard_normal((n_tok, HK, D)) * scale).astype(np.float32)
+    value = (rng.standard_normal((n_tok, HK, D)) * 0.7 + 0.1).astype(np.float32)
+    # round to the input dtype so both sides quantize the same numbers
+    key = torch.from_numpy(key).to(TORCH[dtype]).float().numpy()
+    value = torch.from_numpy(value).to(TORCH[dtype]).float().numpy()
+    slots = rng.permutation(n_blocks * BS)[:n_tok].astype(np.int32)
+    slots[rng.random(n_tok) < 0.1] = -1  # skipped tokens
+    rot_t = workloads.random_orthogonal(rng, D)
+    cents = codebook.centroids(D, 4)
+    mids = ((cents[:-1] + cents[1:]) * np.float32(0.5)).astype(np.float32)
+    return key, value, slots, rot_t, cents, mids
+
+
+def gpu_store(dev, key, value, slots, rot_t, cents, mids, cache0, dtype, layout, nc):
+    cache = to_dev(cache0, dev)
+    ops.store(to_dev(key, dev).to(TORCH[dtype]), to_dev(value, dev).to(TORCH[dtype]), cache,
+              to_dev(slots, dev), to_dev(rot_t, dev), to_dev(mids, dev), to_dev(cents, dev),
+              layout=layout, norm_correction=nc)
+    torch.cuda.synchronize()
+    return cache.cpu().numpy()
+
+
+def rotated(key, rot_t):
+    k = key.astype(np.float64)
+    norm = np.sqrt((k ** 2).sum(-1, keepdims=True))
+    return (k / (norm + 1e-8)) @ rot_t.astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_store_matches_oracle_writer(dev, dtype, layout):
+    n_tok, n_blocks = 300, 24
+    key, value, slots, rot_t, cents, mids = make_inputs(11, n_tok, n_blocks, dtype)
+    aos = layout == "aos"
+    cache0 = np.full((n_blocks, BS, HK, 134), 0xA5, dtype=np.uint8)
+    got = gpu_store(dev, key, value, slots, rot_t, cents, mids, cache0, dtype, layout, not aos)
+    ref = ostore.store(key, value, slots, rot_t, cents, cache0.copy(), block_size=BS, is_aos=aos)
+
+    keep = np.nonzero(slots >= 0)[0]
+    blocks, offs = slots[keep] // BS, slots[keep] % BS
+    gather = OL.gather_aos if aos else OL.gather_soa
+    y = rotated(key[keep], rot_t)
+    near_tie = np.abs(y[..., None] - mids.astype(np.float64)).min(-1) < 1e-6
+    for h in range(HK):
+        gk, gn, gv, gs, gz = gather(got, blocks, offs, h, BS, HK, D)
+        rk, rn, rv, rs, rz = gather(ref, blocks, offs, h, BS, HK, D)
+        assert np.array_equal(gv, rv), "V codes differ"
+        assert np.array_equal(gs, rs) and np.array_equal(gz, rz), "V scale / min differ"
+        diff = gk != rk
+        assert not np.any(diff & ~near_tie[:, h]), "K index differs away from a midpoint"
+        assert np.all(np.abs(gk - rk)[diff] == 1)
+        clean = ~diff.any(-1)  # a tie changes sum(c[idx]^2), so the scalar is checked elsewhere
+        assert np.all(np.abs(gn - rn)[clean] <= np.abs(rn)[clean] * 2.0 ** -10), "K scalar off by > 1 ulp"
+        print(f"head {h}: K index ties {int(diff.sum())}")
+    # bytes outside the written records keep the fill
+    written = np.zeros(cache0.size, dtype=bool)
+    stride = BS * HK * 134
+    for blk, off in zip(blocks.astype(np.int64), offs.astype(np.int64)):
+        for h in range(HK):
+            if aos:
+                b0 = blk * stride + (off * HK + h) * 134
+                written[b0:b0 + 134] = True
+            else:
+                b0 = blk * stride + (off * HK + h) * 128
+                written[b0:b0 + 128] = True
+                meta = blk * stride + BS * HK * 128 + ((h * 3) * BS + off) * 2
+                for f in range(3):
+                    written[meta + 2 * f * BS:meta + 2 * f * BS + 2] = True
+    assert np.array_equal(got.reshape(-1)[~written], cache0.reshape(-1)[~written])
+    assert np.array_equal(ref.reshape(-1)[~written], cache0.reshape(-1)[~written])
+
+
+def test_store_then_decode_round_trip(dev):
+    """Fill a paged cache with the GPU writer (prefill of 3 sequences), then decode it on
+    the GPU and with the oracle."""
+    rng = np.random.default_rng(12)
+    lens = np.array([700, 129, 1500], dtype=np.int32)
+    need = (lens + BS - 1) // BS
+    n_blocks = int(need.sum()) + 2
+    perm = rng.permutation(n_blocks).astype(np.int32)
+    bt = np.zeros((3, int(need.max())), dtype=np.int32)
+    pos = 0
+    for b in range(3):
+        bt[b, :need[b]] = perm[pos:pos + need[b]]
+        pos += need[b]
+    n_tok = int(lens.sum())
+    key, value, _, rot_t, cents, mids = make_inputs(13, n_tok, n_blocks, "bf16")
+    slots = np.concatenate([bt[b, np.arange(lens[b]) // BS] * BS + np.arange(lens[b]) % BS
+                            for b in range(3)]).astype(np.int32)
+    cache0 = np.zeros((n_blocks, BS, HK, 134), dtype=np.uint8)
+    cache = gpu_store(dev, key, value, slots, rot_t, cents, mids, cache0, "bf16", "soa", True)
+    w = workloads.Workload("stored", rng.standard_normal((3, 32, D), dtype=np.float32), cache, bt,
+                           lens, cents, 8, HK)
+    mid = torch.full((3, 32, 8, D + 1), float("nan"), device=dev)
+    ops.stage1(to_dev(w.q_rot, dev), to_dev(cache, dev), to_dev(bt, dev), to_dev(lens, dev),
+               to_dev(w.pair_lut, dev), mid)
+    torch.cuda.synchronize()
+    ref = native.stage1(w.q_rot, cache, bt, lens, cents, 8, num_kv_heads=HK)
+    err = np.nanmax(np.abs(mid.cpu().numpy() - ref))
+    print(f"decode of the stored cache: max-abs {err:.3e}")
+    assert err <= 1e-4
+
+
+def test_reference_store_signature_and_skipped_slots(dev):
+    key, value, slots, rot_t, cents, mids = make_inputs(14, 40, 4, "f16")
+    slots[:] = -1
+    slots[5] = 17
+    cache0 = np.full((4, BS, HK, 134), 0x3C, dtype=np.uint8)
+    cache = to_dev(cache0, dev)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    ops.triton_turboquant_store(t(key).half(), t(value).half(), cache, t(slots), t(rot_t), t(mids),
+                                mse_bits=4, key_packed_size=66, value_quant_bits=4,
+                                centroids=t(cents), norm_correction=True)
+    torch.cuda.synchronize()
+    got = cache.cpu().numpy()
+    ref = ostore.store(key, value, slots, rot_t, cents, cache0.copy(), block_size=BS)
+    changed = got.reshape(-1) != cache0.reshape(-1)
+    assert np.array_equal(changed, ref.reshape(-1) != cache0.reshape(-1)), "only slot 17 is written"
+    with pytest.raises(RuntimeError):
+        ops.triton_turboquant_store(t(key).half(), t(value).half(), cache, t(slots), t(rot_t), t(mids),
+                                    mse_bits=3, key_packed_size=66, value_quant_bits=4)

@@ -16,6 +16,7 @@
 #include "stage1_simple.h"
 #include "stage1_xdl.h"
 #include "stage2.h"
+#include "store.h"
 
 namespace {
 
@@ -336,6 +337,50 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
     if (rc)
         return rc;
     return tq4_stage2(mid_o, seq_lens, out, out_dtype, lse, B, Hq, D, num_kv_splits, stream);
+}
+
+int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
+              const float *rot_t, const float *midpoints, const float *centroids,
+              uint8_t *kv_cache, int N, int Hk, int D, int block_size,
+              int64_t cache_block_stride, int layout, int norm_correction, tq4_stream_t stream) {
+    if (!key || !value || !slot_mapping || !rot_t || !midpoints || !kv_cache)
+        return fail(TQ4_E_INVALID, "tq4_store: null pointer argument");
+    if (norm_correction && !centroids)
+        return fail(TQ4_E_INVALID, "tq4_store: norm_correction requires centroids");
+    if (N < 0 || Hk <= 0 || block_size <= 0)
+        return fail(TQ4_E_INVALID, "tq4_store: N must be >= 0, Hk and block_size positive");
+    if (D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_store: head_dim %d unsupported (128)", D);
+    if (layout != TQ4_LAYOUT_SOA && layout != TQ4_LAYOUT_AOS)
+        return fail(TQ4_E_INVALID, "tq4_store: layout must be 0 (SoA) or 1 (AoS)");
+    const int64_t min_stride = (int64_t)block_size * Hk * tq4::kAosSlot;
+    if (cache_block_stride < min_stride || cache_block_stride % 16)
+        return fail(TQ4_E_INVALID, "tq4_store: requires cache [blocks,%d,%d,134]: block stride %lld",
+                    block_size, Hk, (long long)cache_block_stride);
+    if (!aligned(key, 16) || !aligned(value, 16) || !aligned(kv_cache, 16))
+        return fail(TQ4_E_INVALID, "tq4_store: key, value and kv_cache must be 16-byte aligned");
+    if (N == 0)
+        return ok();
+    const int rows = N * Hk;
+    const dim3 grid((rows + tq4::store::kRows - 1) / tq4::store::kRows);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define TQ4_STORE_LAUNCH(L, T)                                                                       \
+    hipLaunchKernelGGL((tq4::store::store_kernel<L, T>), grid, dim3(tq4::kWave), 0, st,               \
+                       static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, \
+                       midpoints, centroids, kv_cache, rows, Hk, block_size, cache_block_stride,       \
+                       norm_correction)
+    switch (dtype * 2 + layout) {
+    case TQ4_F32 * 2 + 0: TQ4_STORE_LAUNCH(0, float); break;
+    case TQ4_F32 * 2 + 1: TQ4_STORE_LAUNCH(1, float); break;
+    case TQ4_BF16 * 2 + 0: TQ4_STORE_LAUNCH(0, __bf16); break;
+    case TQ4_BF16 * 2 + 1: TQ4_STORE_LAUNCH(1, __bf16); break;
+    case TQ4_F16 * 2 + 0: TQ4_STORE_LAUNCH(0, _Float16); break;
+    case TQ4_F16 * 2 + 1: TQ4_STORE_LAUNCH(1, _Float16); break;
+    default:
+        return fail(TQ4_E_INVALID, "tq4_store: dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
+    }
+#undef TQ4_STORE_LAUNCH
+    return launch_status("store");
 }
 
 }  // extern "C"

@@ -1,4 +1,5 @@
-"""MI355X (gfx950) TurboQuant ``turboquant_4bit_nc`` decode: Stage1 / Stage2 / full step.
+"""MI355X (gfx950) TurboQuant ``turboquant_4bit_nc`` decode: Stage1 / Stage2 / full step,
+and the cache writer.
 
 The compute runs in the HIP library ``libtq4_decode.so`` (C ABI: ``include/tq4_decode.h``);
 this package is the torch-facing host side with the reference harness's call shapes.
@@ -8,7 +9,8 @@ from . import codebook, layout, workloads  # noqa: F401  (host-side, no GPU need
 __all__ = [
     "codebook", "layout", "workloads", "ops", "stage1", "stage2", "full_decode",
     "rotate_query", "pair_lut_device", "launch_tq4_v2_stage1", "launch_soa_v1_stage1",
-    "launch_aos_v1_stage1", "launch_stage2", "ext", "DecodeWorkspace", "Tq4Error",
+    "launch_aos_v1_stage1", "launch_stage2", "ext", "DecodeWorkspace", "Tq4Error", "store",
+    "triton_turboquant_store",
 ]
 
 

@@ -23,6 +23,7 @@ EXPORTS = (
     "tq4_rotate_query",
     "tq4_build_pair_lut",
     "tq4_full_decode",
+    "tq4_store",
     "tq4_last_error",
     "tq4_abi_version",
 )
@@ -38,6 +39,7 @@ _SIGS = {
     "tq4_build_pair_lut": [_p, _p, _i, _p],
     "tq4_full_decode": [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i,
                         _i, _i64, _i, _i, _f, _p],
+    "tq4_store": [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _p],
     "tq4_last_error": [],
     "tq4_abi_version": [],
 }

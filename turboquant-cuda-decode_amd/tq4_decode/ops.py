@@ -12,6 +12,9 @@ Reference call shapes kept here:
 * ``launch_soa_v1_stage1`` / ``launch_aos_v1_stage1(q_rot, kv_cache, block_table, seq_lens,
   centroids, mid_o)`` -- ``baseline/triton_v1.py:90-203``
 * ``launch_stage2(mid_o, seq_lens, output, lse)`` -- ``baseline/stage2.py:58-81``
+* ``triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits,
+  key_packed_size, value_quant_bits, key_fp8=False, centroids=None, norm_correction=False)``
+  -- ``reference/soa_store.py:381-524`` (4-bit keys and values)
 * ``ext`` -- object with the CUDA-extension names ``tq4_cuda_v1 .. tq4_cuda_v9``,
   ``tq4_cuda_v7_stage1 / _stage2 / _full`` (``cuda/tq4_cuda_v7_bind.cpp:3-20``), so
   ``cuda_ext = tq4_decode.ext`` drops into ``benchmarks/stage1.py`` / ``full_decode.py``.
@@ -144,6 +147,47 @@ def rotate_query(query, rotation_t, q_rot=None):
     return q_rot
 
 
+def store(key, value, kv_cache, slot_mapping, rotation_t, midpoints, centroids=None, *,
+          layout="soa", norm_correction=True):
+    """Quantize ``key`` / ``value`` ``[N, Hk, D]`` and write token ``i`` into cache slot
+    ``slot_mapping[i]`` (negative slots are skipped); returns ``kv_cache``.
+
+    K: 4-bit Lloyd-Max indices of ``(k / (||k|| + 1e-8)) @ rotation_t`` against
+    ``midpoints`` [15]; stored scalar ``fp16(||k|| / ||c[idx]||)`` with
+    ``norm_correction`` (needs ``centroids`` [16]), else ``fp16(||k||)``.  V: 4-bit
+    uniform codes, fp16 scale and fp16 min.
+    """
+    _require(key.is_cuda and key.dtype in DTYPES and key.is_contiguous(), "invalid key")
+    _require(value.dtype == key.dtype and value.is_contiguous() and value.shape == key.shape,
+             "value must match key (shape, dtype, contiguous)")
+    _require(key.dim() == 3 and key.size(2) == HEAD_DIM, f"key must be [N, Hk, {HEAD_DIM}]")
+    _check_tensor(kv_cache, "kv_cache", torch.uint8)
+    _check_tensor(slot_mapping, "slot_mapping", torch.int32)
+    _check_tensor(rotation_t, "rotation_t", torch.float32)
+    _check_tensor(midpoints, "midpoints", torch.float32)
+    _require(midpoints.numel() == 15, "4-bit keys need 15 midpoints")
+    _require(tuple(rotation_t.shape) == (HEAD_DIM, HEAD_DIM), f"rotation must be [{HEAD_DIM}, {HEAD_DIM}]")
+    if norm_correction:
+        _require(centroids is not None, "norm_correction=True requires centroids")
+    if centroids is not None:
+        _check_tensor(centroids, "centroids", torch.float32)
+        _require(centroids.numel() == 16, "4-bit keys need 16 centroids")
+    N, Hk, D = key.shape
+    _require(kv_cache.dim() == 4 and kv_cache.size(2) == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
+    _require(kv_cache.size(3) == slot_bytes(D), f"requires slot_size={slot_bytes(D)}")
+    _require(slot_mapping.numel() == N, "slot_mapping must have one entry per token")
+    devs = {t.device for t in (key, value, kv_cache, slot_mapping, rotation_t, midpoints)}
+    _require(len(devs) == 1, "all tensors must be on the same device")
+    rc = _lib.load().tq4_store(
+        key.data_ptr(), value.data_ptr(), DTYPES[key.dtype], slot_mapping.data_ptr(),
+        rotation_t.data_ptr(), midpoints.data_ptr(),
+        centroids.data_ptr() if centroids is not None else None, kv_cache.data_ptr(), N, Hk, D,
+        kv_cache.size(1), kv_cache.stride(0), _layout_id(layout), int(bool(norm_correction)),
+        _stream(key.device))
+    _lib.check(rc, "tq4_store")
+    return kv_cache
+
+
 class DecodeWorkspace:
     """Preallocated buffers of one full decode step (fixed shapes, reusable)."""
 
@@ -214,6 +258,19 @@ def launch_aos_v1_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, mid_
 def launch_stage2(mid_o, seq_lens, output, lse):
     """Stage2 with the ``baseline/stage2.py:58-63`` signature (writes in place)."""
     stage2(mid_o, seq_lens, output, lse)
+
+
+def triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits,
+                            key_packed_size, value_quant_bits, key_fp8=False, centroids=None,
+                            norm_correction=False):
+    """SoA cache writer with the ``reference/soa_store.py:381-397`` signature (MSE path,
+    4-bit keys and values; the FP8-key path and other bit widths are not built)."""
+    if key_fp8:
+        raise NotImplementedError("FP8 keys (the k8v4 presets) are not built")
+    _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
+    _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
+    store(key, value, kv_cache, slot_mapping, PiT, midpoints, centroids, layout="soa",
+          norm_correction=norm_correction)
 
 
 class _CudaExtCompat:
