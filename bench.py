@@ -114,6 +114,45 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
+def store_times(dev, flush, timer, reps=30):
+    """Cache writer (tq4_store, SoA, bf16 K/V, norm correction) cold: one decode step
+    (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  Bytes per (token,
+    kv-head): 2 x 256 read + 134 written, plus 4 of slot mapping per token."""
+    import numpy as np
+    import torch
+
+    from tq4_decode import codebook, ops, workloads
+
+    rng = np.random.default_rng(7)
+    cents = codebook.centroids(128, 4)
+    mids = ((cents[:-1] + cents[1:]) * np.float32(0.5)).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    rot, c, m = t(workloads.random_orthogonal(rng, 128)), t(cents), t(mids)
+    out = {}
+    for name, n_tok in (("decode_b64", 64), ("prefill_n8192", 8192)):
+        key = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
+        val = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
+        n_blocks = (n_tok + 15) // 16 + 4
+        cache = torch.zeros(n_blocks, 16, 8, 134, dtype=torch.uint8, device=dev)
+        slots = torch.randperm(n_blocks * 16, device=dev)[:n_tok].to(torch.int32)
+        times = []
+        for i in range(reps + 3):
+            flush.sum()
+            a, b = timer.pair()
+            timer.record(a)
+            ops.store(key, val, cache, slots, rot, m, c)
+            timer.record(b)
+            torch.cuda.synchronize()
+            if i >= 3:
+                times.append(timer.elapsed_ms(a, b) * 1e3)
+            timer.destroy(a, b)
+        us = statistics.median(times)
+        nbytes = n_tok * 8 * (2 * 256 + 134) + n_tok * 4
+        out[f"{name}_us"] = round(us, 2)
+        out[f"{name}_GBps"] = round(nbytes / us / 1e3, 1)
+    return out
+
+
 def cpu_baseline(w, threads: int, repeats: int = 3):
     from oracle import native
 
@@ -244,6 +283,8 @@ def main() -> int:
             var[f"{layout}_{kernel}_cold_us"] = round(vm * 1e3, 2)
             var[f"{layout}_{kernel}_warm_us"] = round(warm_time(layout, kernel) * 1e3, 2)
         result["variants"] = var
+    if not args.no_variants:
+        result["store"] = store_times(dev, flush, timer)
     if args.calibrate_copy:
         src = torch.empty(1 << 26, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)

@@ -57,13 +57,19 @@ def test_reference_stage2_call_shapes(dev):
     assert torch.equal(out, out7) and torch.equal(lse, lse7)
 
 
-def test_rotate_query_matches_fp64(dev):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows", [1, 64, 65, 120, 8192])
+def test_rotate_query_matches_fp64(dev, dtype, rows):
+    """Matrix-core rotation (f16 hi/lo splits) vs an fp64 matmul of the same inputs;
+    row counts around the 64-row workgroup tile."""
     rng = np.random.default_rng(204)
-    query = rng.standard_normal((40, 3, 128)).astype(np.float16)
+    q = torch.from_numpy(rng.standard_normal((rows, 128)).astype(np.float32)).to(dtype)
     rot = workloads.random_orthogonal(rng, 128)
-    got = ops.rotate_query(to_dev(query, dev), to_dev(rot, dev)).cpu().numpy()
-    ref = query.astype(np.float64) @ rot.astype(np.float64)
-    assert np.abs(got - ref).max() <= 2e-5
+    got = ops.rotate_query(q.to(dev), to_dev(rot, dev)).cpu().numpy()
+    ref = q.double().numpy() @ rot.astype(np.float64)
+    err = np.abs(got - ref).max()
+    print(f"rotation max-abs {err:.3e}")
+    assert err <= 2e-5
 
 
 def test_full_b256_ctx2048_bf16(dev):

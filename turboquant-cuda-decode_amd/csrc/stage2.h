@@ -34,6 +34,8 @@ __global__ __launch_bounds__(kWave) void stage2_kernel(const float *__restrict__
     mx = wave_max(mx);
 
     float a0 = 0.f, a1 = 0.f, wsum = 0.f;
+    // unrolled so that several split rows are loaded at a time
+#pragma unroll 8
     for (int s = 0; s < live; ++s) {
         const float *row = base + (int64_t)s * (kHeadDim + 1);
         const float w = expf(row[kHeadDim] - mx);
@@ -49,33 +51,84 @@ __global__ __launch_bounds__(kWave) void stage2_kernel(const float *__restrict__
         lse[(int64_t)b * num_q_heads + h] = mx + logf(wsum);
 }
 
-// q_rot[r, n] = sum_k float(query[r, k]) * rot_t[k, n]; 128 threads (one per output
-// column) per group of kRotRows rows; the query rows are staged in LDS.
-constexpr int kRotRows = 16;
+// Rotation on the f16 matrix cores: q_rot = query @ rot_t with rot_t split into f16
+// hi + lo parts (hi + lo = rot_t to ~2^-22), and for fp32 queries the query too
+// (products hi*hi + hi*lo + lo*hi; fp16 and bf16 queries are taken as f16, exact for the
+// magnitudes of attention queries).  A workgroup of 4 waves stages rot_t^T as f16 parts in
+// LDS (2 x 32 KB) and each wave rotates 16 rows: lane (n, g) feeds A[row n][k 8g .. 8g+7]
+// and B[k 8g .. 8g+7][col n] of v_mfma_f32_16x16x32_f16 and gets D[rows 4g .. 4g+3][col n].
+constexpr int kRotWaves = 4;
+constexpr int kRotMfmaRows = 16 * kRotWaves;  // rows per workgroup
+constexpr int kRotPt = kHeadDim + 8;           // LDS row of rot_t^T (halves), 16-byte aligned
+typedef _Float16 rot_half8 __attribute__((ext_vector_type(8)));
+
 template <typename InT>
-__global__ __launch_bounds__(kHeadDim) void rotate_query_kernel(const InT *__restrict__ query,
-                                                               const float *__restrict__ rot_t,
-                                                               float *__restrict__ q_rot,
-                                                               int rows) {
-    __shared__ float qs[kRotRows][kHeadDim];
-    const int n = threadIdx.x;
-    const int r0 = blockIdx.x * kRotRows;
-    const int nr = min(kRotRows, rows - r0);
-    for (int i = 0; i < nr; ++i)
-        qs[i][n] = to_float<InT>(query[(int64_t)(r0 + i) * kHeadDim + n]);
-    __syncthreads();
-    float acc[kRotRows];
+__device__ __forceinline__ void rot_a_operands(const InT *p, rot_half8 &hi, rot_half8 &lo) {
 #pragma unroll
-    for (int i = 0; i < kRotRows; ++i)
-        acc[i] = 0.f;
-    for (int k = 0; k < kHeadDim; ++k) {
-        const float w = rot_t[k * kHeadDim + n];
-#pragma unroll
-        for (int i = 0; i < kRotRows; ++i)
-            acc[i] += qs[i][k] * w;
+    for (int j = 0; j < 8; ++j) {
+        const float x = to_float<InT>(p[j]);
+        hi[j] = (_Float16)x;
+        lo[j] = sizeof(InT) == 4 ? (_Float16)(x - (float)hi[j]) : (_Float16)0.f;
     }
-    for (int i = 0; i < nr; ++i)
-        q_rot[(int64_t)(r0 + i) * kHeadDim + n] = acc[i];
+}
+
+template <typename InT>
+__global__ __launch_bounds__(kWave *kRotWaves) void rotate_mfma_kernel(const InT *__restrict__ query,
+                                                                        const float *__restrict__ rot_t,
+                                                                        float *__restrict__ q_rot, int rows,
+                                                                        const float *__restrict__ centroids,
+                                                                        float *__restrict__ pair_lut) {
+    // optional side task of the first workgroup: the pair LUT (row lo * 16 + hi = (c[lo], c[hi]))
+    if (pair_lut && blockIdx.x == 0 && threadIdx.x < 256) {
+        pair_lut[2 * threadIdx.x] = centroids[threadIdx.x / 16];
+        pair_lut[2 * threadIdx.x + 1] = centroids[threadIdx.x % 16];
+    }
+    __shared__ __align__(16) _Float16 pt_hi[kHeadDim * kRotPt];  // [col][k]
+    __shared__ __align__(16) _Float16 pt_lo[kHeadDim * kRotPt];
+    // thread (c, kg): rot_t[8kg .. 8kg+7][c] (coalesced over c) -> one 16-byte LDS write each
+    for (int i = threadIdx.x; i < kHeadDim * (kHeadDim / 8); i += blockDim.x) {
+        const int c = i % kHeadDim, kg = i / kHeadDim;
+        rot_half8 h, l;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float w = rot_t[(8 * kg + j) * kHeadDim + c];
+            h[j] = (_Float16)w;
+            l[j] = (_Float16)(w - (float)h[j]);
+        }
+        *reinterpret_cast<rot_half8 *>(pt_hi + c * kRotPt + 8 * kg) = h;
+        *reinterpret_cast<rot_half8 *>(pt_lo + c * kRotPt + 8 * kg) = l;
+    }
+    __syncthreads();
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int n = lane & 15, g = lane >> 4;
+    const int r0 = blockIdx.x * kRotMfmaRows + 16 * wave;
+    if (r0 >= rows)
+        return;
+    const int ra = min(r0 + n, rows - 1);  // rows past the end repeat the last one (not stored)
+    rot_half8 a_hi[4], a_lo[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+        rot_a_operands<InT>(query + (int64_t)ra * kHeadDim + 32 * kb + 8 * g, a_hi[kb], a_lo[kb]);
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const int off = (16 * cb + n) * kRotPt + 32 * kb + 8 * g;
+            const rot_half8 b_hi = *reinterpret_cast<const rot_half8 *>(pt_hi + off);
+            const rot_half8 b_lo = *reinterpret_cast<const rot_half8 *>(pt_lo + off);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[kb], b_hi, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[kb], b_lo, acc, 0, 0, 0);
+            if constexpr (sizeof(InT) == 4)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[kb], b_hi, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = r0 + 4 * g + i;
+            if (r < rows)
+                q_rot[(int64_t)r * kHeadDim + 16 * cb + n] = acc[i];
+        }
+    }
 }
 
 __global__ void pair_lut_kernel(const float *__restrict__ cents, float *__restrict__ lut, int n) {

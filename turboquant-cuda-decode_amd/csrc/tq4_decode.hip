@@ -142,7 +142,6 @@ template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_
                        log2_int(a.bs), a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
 
-// The 16x16x32 kernel is compiled for 2 waves per SIMD (its register budget: 256 VGPRs).
 // Waves per SIMD the 16x16x32 kernel is built for.  Two: the SoA G=4 kernel also fits
 // three (168 VGPRs, a 5-split LDS image), but runs slower that way.
 #ifndef TQ4_XDL_WAVES_PER_SIMD
@@ -152,10 +151,15 @@ template <int LAYOUT, int G> constexpr int xdl_waves_per_simd() {
     return LAYOUT == 0 && G == 4 ? TQ4_XDL_WAVES_PER_SIMD : 2;
 }
 
-template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
+template <int LAYOUT, int G> int xdl_waves(const Stage1Args &a) {
     static int slots = 0;
     const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>()>;
-    const dim3 grid(a.Hk, waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots), a.B);
+    return waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots);
+}
+
+template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
+    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>()>;
+    const dim3 grid(a.Hk, xdl_waves<LAYOUT, G>(a), a.B);
     hipLaunchKernelGGL(kernel, grid, dim3(tq4::kWave), 0, st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
                        a.mid_o, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks, a.stride, a.S,
                        a.scale * tq4::kLog2e);
@@ -203,6 +207,17 @@ template <int LAYOUT> int dispatch_xdl(const Stage1Args &a, hipStream_t st) {
     return launch_status("stage1_xdl");
 }
 
+// Waves per (sequence, kv-head) the auto Stage1 kernel runs with (0 when it is not the
+// 16x16x32 kernel).
+int auto_xdl_waves(const Stage1Args &a) {
+    if (!mfma_applies(a))
+        return 0;
+    const bool g4 = a.Hq / a.Hk == 4;
+    if (a.layout == TQ4_LAYOUT_SOA)
+        return g4 ? xdl_waves<0, 4>(a) : xdl_waves<0, 8>(a);
+    return g4 ? xdl_waves<1, 4>(a) : xdl_waves<1, 8>(a);
+}
+
 int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     int rc = check_stage1(a);
     if (rc)
@@ -217,6 +232,36 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     if (kernel == TQ4_KERNEL_XDL)
         return a.layout == TQ4_LAYOUT_SOA ? dispatch_xdl<0>(a, st) : dispatch_xdl<1>(a, st);
     return fail(TQ4_E_INVALID, "tq4_stage1_ex: unknown kernel id %d", kernel);
+}
+
+int rotate_query(const void *query, int query_dtype, const float *rot_t, float *q_rot, int rows,
+                 int D, const float *centroids, float *pair_lut, hipStream_t st) {
+    if (!query || !rot_t || !q_rot)
+        return fail(TQ4_E_INVALID, "tq4_rotate_query: null pointer argument");
+    if (rows <= 0)
+        return fail(TQ4_E_INVALID, "tq4_rotate_query: rows must be positive");
+    if (D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_rotate_query: head_dim %d unsupported (128)", D);
+    if (!aligned(query, 16))
+        return fail(TQ4_E_INVALID, "tq4_rotate_query: query must be 16-byte aligned");
+    const dim3 grid((rows + tq4::kRotMfmaRows - 1) / tq4::kRotMfmaRows), block(tq4::kWave * tq4::kRotWaves);
+    switch (query_dtype) {
+    case TQ4_F32:
+        hipLaunchKernelGGL(tq4::rotate_mfma_kernel<float>, grid, block, 0, st,
+                           static_cast<const float *>(query), rot_t, q_rot, rows, centroids, pair_lut);
+        break;
+    case TQ4_BF16:
+        hipLaunchKernelGGL(tq4::rotate_mfma_kernel<__bf16>, grid, block, 0, st,
+                           static_cast<const __bf16 *>(query), rot_t, q_rot, rows, centroids, pair_lut);
+        break;
+    case TQ4_F16:
+        hipLaunchKernelGGL(tq4::rotate_mfma_kernel<_Float16>, grid, block, 0, st,
+                           static_cast<const _Float16 *>(query), rot_t, q_rot, rows, centroids, pair_lut);
+        break;
+    default:
+        return fail(TQ4_E_INVALID, "tq4_rotate_query: query_dtype must be 0, 1 or 2");
+    }
+    return launch_status("rotate_query");
 }
 
 }  // namespace
@@ -279,31 +324,8 @@ int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_d
 
 int tq4_rotate_query(const void *query, int query_dtype, const float *rot_t, float *q_rot,
                      int rows, int D, tq4_stream_t stream) {
-    if (!query || !rot_t || !q_rot)
-        return fail(TQ4_E_INVALID, "tq4_rotate_query: null pointer argument");
-    if (rows <= 0)
-        return fail(TQ4_E_INVALID, "tq4_rotate_query: rows must be positive");
-    if (D != tq4::kHeadDim)
-        return fail(TQ4_E_UNSUPPORTED, "tq4_rotate_query: head_dim %d unsupported (128)", D);
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid((rows + tq4::kRotRows - 1) / tq4::kRotRows);
-    switch (query_dtype) {
-    case TQ4_F32:
-        hipLaunchKernelGGL(tq4::rotate_query_kernel<float>, grid, dim3(tq4::kHeadDim), 0, st,
-                           static_cast<const float *>(query), rot_t, q_rot, rows);
-        break;
-    case TQ4_BF16:
-        hipLaunchKernelGGL(tq4::rotate_query_kernel<__bf16>, grid, dim3(tq4::kHeadDim), 0, st,
-                           static_cast<const __bf16 *>(query), rot_t, q_rot, rows);
-        break;
-    case TQ4_F16:
-        hipLaunchKernelGGL(tq4::rotate_query_kernel<_Float16>, grid, dim3(tq4::kHeadDim), 0, st,
-                           static_cast<const _Float16 *>(query), rot_t, q_rot, rows);
-        break;
-    default:
-        return fail(TQ4_E_INVALID, "tq4_rotate_query: query_dtype must be 0, 1 or 2");
-    }
-    return launch_status("rotate_query");
+    return rotate_query(query, query_dtype, rot_t, q_rot, rows, D, nullptr, nullptr,
+                        reinterpret_cast<hipStream_t>(stream));
 }
 
 int tq4_build_pair_lut(const float *centroids, float *pair_lut, int n_centroids,
@@ -325,18 +347,25 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
                     int B, int Hq, int Hk, int D, int block_size, int max_blocks_per_seq,
                     int64_t cache_block_stride, int num_kv_splits, int layout,
                     float attn_scale, tq4_stream_t stream) {
-    int rc = tq4_rotate_query(query, query_dtype, rot_t, q_rot_ws, B * Hq, D, stream);
+    if (!centroids || !pair_lut_ws)
+        return fail(TQ4_E_INVALID, "tq4_full_decode: null pointer argument");
+    // one launch rotates the query and writes the pair LUT
+    int rc = rotate_query(query, query_dtype, rot_t, q_rot_ws, B * Hq, D, centroids, pair_lut_ws,
+                          reinterpret_cast<hipStream_t>(stream));
     if (rc)
         return rc;
-    rc = tq4_build_pair_lut(centroids, pair_lut_ws, 16, stream);
+    // When the Stage1 kernel gives each (sequence, kv-head) one wave anyway, that wave runs
+    // the whole sequence as one split: the same attention (up to rounding), without writing
+    // and re-reading num_kv_splits rows per head; Stage2 then only converts the row.
+    Stage1Args a{q_rot_ws, kv_cache, block_table, seq_lens, pair_lut_ws, mid_o, B, Hq, Hk, D,
+                 block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
+                 attn_scale};
+    if (num_kv_splits > 1 && check_stage1(a) == TQ4_OK && auto_xdl_waves(a) == 1)
+        a.S = 1;
+    rc = run_stage1(a, TQ4_KERNEL_AUTO, reinterpret_cast<hipStream_t>(stream));
     if (rc)
         return rc;
-    rc = tq4_stage1(q_rot_ws, kv_cache, block_table, seq_lens, pair_lut_ws, mid_o, B, Hq, Hk, D,
-                    block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
-                    attn_scale, stream);
-    if (rc)
-        return rc;
-    return tq4_stage2(mid_o, seq_lens, out, out_dtype, lse, B, Hq, D, num_kv_splits, stream);
+    return tq4_stage2(mid_o, seq_lens, out, out_dtype, lse, B, Hq, D, a.S, stream);
 }
 
 int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
