@@ -153,6 +153,38 @@ def store_times(dev, flush, timer, reps=30):
     return out
 
 
+def full_decode_time(dev, flush, timer, reps=30):
+    """Whole decode step (fp16 query -> rotation + pair LUT -> Stage1 -> Stage2 -> fp16
+    out) at B=256 x ctx 2048, 32/8 heads, 16 splits, cold.  Bytes: KV of every token
+    and kv-head + query in + output and LSE out + block table."""
+    import numpy as np
+    import torch
+
+    from tq4_decode import ops, workloads
+
+    w = workloads.full_b256_ctx2048()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    args = (t(w.query), t(w.rotation_t), t(w.kv_cache), t(w.block_table), t(w.seq_lens),
+            t(w.centroids), w.num_kv_splits)
+    ws = ops.DecodeWorkspace(w.batch, w.num_q_heads, w.num_kv_splits, dev, torch.float16)
+    times = []
+    for i in range(reps + 3):
+        flush.sum()
+        a, b = timer.pair()
+        timer.record(a)
+        ops.full_decode(*args, workspace=ws)
+        timer.record(b)
+        torch.cuda.synchronize()
+        if i >= 3:
+            times.append(timer.elapsed_ms(a, b) * 1e3)
+        timer.destroy(a, b)
+    us = statistics.median(times)
+    nbytes = (int(w.seq_lens.sum()) * w.num_kv_heads * 134 + w.query.nbytes + w.query.nbytes
+              + w.batch * w.num_q_heads * 4 + w.block_table.nbytes)
+    return {"workload": "b256_ctx2048_32q8kv_s16_fp16", "us": round(us, 2),
+            "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes}
+
+
 def cpu_baseline(w, threads: int, repeats: int = 3):
     from oracle import native
 
@@ -285,6 +317,7 @@ def main() -> int:
         result["variants"] = var
     if not args.no_variants:
         result["store"] = store_times(dev, flush, timer)
+        result["full_decode"] = full_decode_time(dev, flush, timer)
     if args.calibrate_copy:
         src = torch.empty(1 << 26, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)

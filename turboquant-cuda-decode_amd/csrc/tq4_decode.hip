@@ -391,10 +391,11 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
     if (N == 0)
         return ok();
     const int rows = N * Hk;
-    const dim3 grid((rows + tq4::store::kRows - 1) / tq4::store::kRows);
+    const int per_group = tq4::store::kRows * tq4::store::kWaves;
+    const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, tq4::store::kMaxGroups));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define TQ4_STORE_LAUNCH(L, T)                                                                       \
-    hipLaunchKernelGGL((tq4::store::store_kernel<L, T>), grid, dim3(tq4::kWave), 0, st,               \
+    hipLaunchKernelGGL((tq4::store::store_kernel<L, T>), grid, dim3(tq4::kWave * tq4::store::kWaves), 0, st, \
                        static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, \
                        midpoints, centroids, kv_cache, rows, Hk, block_size, cache_block_stride,       \
                        norm_correction)
