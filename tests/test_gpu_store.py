@@ -95,6 +95,60 @@ def test_store_matches_oracle_writer(dev, dtype, layout):
     assert np.array_equal(ref.reshape(-1)[~written], cache0.reshape(-1)[~written])
 
 
+def check_against_oracle(dev, key, value, slots, rot_t, cents, n_blocks, dtype="f32"):
+    mids = ((cents[:-1] + cents[1:]) * np.float32(0.5)).astype(np.float32)
+    cache0 = np.zeros((n_blocks, BS, HK, 134), dtype=np.uint8)
+    got = gpu_store(dev, key, value, slots, rot_t, cents, mids, cache0, dtype, "soa", True)
+    ref = ostore.store(key, value, slots, rot_t, cents, cache0.copy(), block_size=BS)
+    keep = np.nonzero(slots >= 0)[0]
+    blocks, offs = slots[keep] // BS, slots[keep] % BS
+    y = rotated(key[keep], rot_t)
+    near_tie = np.abs(y[..., None] - mids.astype(np.float64)).min(-1) < 1e-6
+    ties = 0
+    for h in range(HK):
+        gk, gn, gv, gs, gz = OL.gather_soa(got, blocks, offs, h, BS, HK, D)
+        rk, rn, rv, rs, rz = OL.gather_soa(ref, blocks, offs, h, BS, HK, D)
+        assert np.array_equal(gv, rv), "V codes differ"
+        assert np.array_equal(gs, rs) and np.array_equal(gz, rz), "V scale / min differ"
+        diff = gk != rk
+        assert not np.any(diff & ~near_tie[:, h]), "K index differs away from a midpoint"
+        clean = ~diff.any(-1)
+        assert np.all(np.abs(gn - rn)[clean] <= np.abs(rn)[clean] * 2.0 ** -10)
+        ties += int(diff.sum())
+    return ties
+
+
+def test_store_codebook_with_close_midpoints(dev):
+    """Two midpoints closer than a bucketize table cell: the writer counts midpoints one by
+    one instead of using the table; indices still match the oracle's."""
+    rng = np.random.default_rng(15)
+    n_tok = 200
+    key = rng.standard_normal((n_tok, HK, D)).astype(np.float32)
+    value = rng.standard_normal((n_tok, HK, D)).astype(np.float32)
+    slots = rng.permutation(16 * BS)[:n_tok].astype(np.int32)
+    cents = codebook.centroids(D, 4).astype(np.float32).copy()
+    cents[7], cents[9] = cents[8] - np.float32(1e-4), cents[8] + np.float32(1e-4)
+    mids = (cents[:-1] + cents[1:]) * np.float32(0.5)
+    assert np.all(np.diff(cents) > 0) and mids[8] - mids[7] < 2e-4  # midpoints 7, 8 1e-4 apart
+    ties = check_against_oracle(dev, key, value, slots, workloads.random_orthogonal(rng, D), cents, 16)
+    print(f"K index ties {ties}")
+
+
+def test_store_values_on_code_boundaries(dev):
+    """V rows on a half-step grid: many quotients (v - min) / scale + 0.5 land exactly on an
+    integer, where the reciprocal shortcut could round to the other code."""
+    rng = np.random.default_rng(16)
+    n_tok = 256
+    key = rng.standard_normal((n_tok, HK, D)).astype(np.float32)
+    steps = rng.integers(0, 31, (n_tok, HK, D)).astype(np.float32)
+    steps[..., 0], steps[..., 1] = 0, 30  # range = 15 steps -> scale = step
+    step = rng.choice(np.float32([0.5, 0.1, 0.3, 1.7, 3e-3]), (n_tok, HK, 1)).astype(np.float32)
+    value = (steps * np.float32(0.5) * step - np.float32(1.3)).astype(np.float32)
+    slots = rng.permutation(16 * BS)[:n_tok].astype(np.int32)
+    cents = codebook.centroids(D, 4)
+    check_against_oracle(dev, key, value, slots, workloads.random_orthogonal(rng, D), cents, 16)
+
+
 def test_store_then_decode_round_trip(dev):
     """Fill a paged cache with the GPU writer (prefill of 3 sequences), then decode it on
     the GPU and with the oracle."""

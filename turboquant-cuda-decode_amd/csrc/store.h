@@ -15,8 +15,10 @@
 // 134-byte slot (t, h) = K bytes | fp16 norm | V bytes | fp16 scale | fp16 min.
 //
 // A workgroup of 8 waves stages 16 * PiT^T in LDS as f16 hi + lo parts once, then its
-// waves walk the rows 16 at a time (grid-stride).  Lane (n, g) = (lane % 16, lane / 16)
-// loads dims 32g .. 32g+31 of row n of K and V.  The rotation is the transposed product
+// waves walk the rows 16 at a time (grid-stride); the first tile's K and V loads are issued
+// before the staging, each later tile's at the end of the previous one (fp32 V, 32 VGPRs,
+// where it is used).  Lane (n, g) = (lane % 16, lane / 16) loads dims 32g .. 32g+31 of
+// row n of K and V.  The rotation is the transposed product
 // y^T = PiT^T x_hat^T on v_mfma_f32_16x16x32_f16, with operands and x_hat (scaled by 16,
 // keeping the lo parts out of f16 denormals) split into f16 hi + lo (products hi*hi +
 // hi*lo + lo*hi, ~fp32 accurate).  Two index maps make every operand and result
@@ -27,6 +29,19 @@
 //                registers of lane (n, g) are y[row n][32g + 4cb + i] -- its own 32 dims
 //                in order, ready for bucketize and packing.
 // Reductions over a row's four lanes (n + 16g) use permlane swaps.
+//
+// Bucketize: the workgroup builds a cell table over the midpoints' span (kCells cells of
+// width w, two spare cells each side).  Cell k's window is [y0 + kw - w/64, y0 + (k+1)w +
+// w/64]; its entry holds the one midpoint inside the window (NaN if none), the number of
+// midpoints below the window, and c^2 at those two indices.  A y whose computed cell is k
+// lies inside window k (the computed cell coordinate is off by < 1e-3 cells for |y| < 100;
+// beyond the span the edge cells hold for every y), so count(midpoints <= y) = base +
+// (y >= mid): one LDS read and one compare per element instead of 15.  When some window
+// holds two midpoints (a codebook with a gap under ~w) the kernel counts all 15 instead.
+//
+// V codes: (v - min) * (1 / scale) is within 2^-18 of the fp32 quotient (v - min) / scale
+// for quotients below 16, so the code (truncation of quotient + 0.5) is the same unless
+// quotient + 0.5 lies within 2^-16 of an integer; such elements take the division.
 #pragma once
 #include "tq4_device.h"
 
@@ -35,7 +50,8 @@ namespace store {
 
 constexpr int kWaves = 8;           // waves per workgroup
 constexpr int kRows = 16;           // rows per wave step
-constexpr int kMaxGroups = 512;     // 2 resident workgroups per CU (64 KB LDS each)
+constexpr int kMaxGroups = 512;     // two resident workgroups per CU (LDS), 4 waves per SIMD
+constexpr int kCells = 128;         // bucketize table cells
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 // LDS image of PiT^T: row c (an output dim) holds PiT[0 .. 127][c] as 16 chunks of 8
@@ -66,45 +82,37 @@ __device__ __forceinline__ float row_max(float x) {
     return fmaxf(bitsf(r[0]), bitsf(r[1]));
 }
 
-// 32 consecutive elements as fp32 (16-byte aligned source).
-template <class T> __device__ __forceinline__ void load_chunk(float (&x)[32], const T *p) {
-    if constexpr (sizeof(T) == 4) {
+// 32 consecutive elements of one row as raw 16-byte words (16-byte aligned source).
+template <class T> struct Chunk {
+    uint4 u[2 * sizeof(T)];
+};
+template <class T> __device__ __forceinline__ void load_raw(Chunk<T> &c, const T *p, bool ok) {
+    if (ok) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 v = reinterpret_cast<const float4 *>(p)[i];
-            x[4 * i] = v.x;
-            x[4 * i + 1] = v.y;
-            x[4 * i + 2] = v.z;
-            x[4 * i + 3] = v.w;
-        }
+        for (int i = 0; i < 2 * (int)sizeof(T); ++i)
+            c.u[i] = reinterpret_cast<const uint4 *>(p)[i];
     } else {
-        typedef T t8 __attribute__((ext_vector_type(8)));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const t8 v = reinterpret_cast<const t8 *>(p)[i];
+        for (int i = 0; i < 2 * (int)sizeof(T); ++i)
+            c.u[i] = uint4{0u, 0u, 0u, 0u};
+    }
+}
+template <class T> __device__ __forceinline__ void to_floats(float (&x)[32], const Chunk<T> &c) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                x[8 * i + j] = (float)v[j];
+    for (int i = 0; i < 2 * (int)sizeof(T); ++i) {
+        const uint32_t w[4] = {c.u[i].x, c.u[i].y, c.u[i].z, c.u[i].w};
+#pragma unroll
+        for (int e = 0; e < 16 / (int)sizeof(T); ++e) {
+            if constexpr (sizeof(T) == 4)
+                x[4 * i + e] = __builtin_bit_cast(float, w[e]);
+            else
+                x[8 * i + e] = (float)__builtin_bit_cast(T, (uint16_t)(w[e / 2] >> (16 * (e % 2))));
         }
     }
 }
 
 __device__ __forceinline__ uint16_t half_bits(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
-}
-
-// Two 4-bit codes per byte, low nibble = even element: 32 codes -> 16 bytes.
-__device__ __forceinline__ uint4 pack32(const int (&c)[32]) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t v = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            v |= (uint32_t)((c[8 * i + 2 * j] & 15) | ((c[8 * i + 2 * j + 1] & 15) << 4)) << (8 * j);
-        w[i] = v;
-    }
-    return uint4{w[0], w[1], w[2], w[3]};
 }
 
 // 2-byte stores of 16 bytes at a 2-byte aligned address (AoS slots).
@@ -119,17 +127,31 @@ __device__ __forceinline__ void store16_a2(uint8_t *p, uint4 v) {
 }
 
 template <int LAYOUT, class T>
-__global__ __launch_bounds__(kWave *kWaves) void store_kernel(const T *__restrict__ key, const T *__restrict__ value,
-                                                      const int32_t *__restrict__ slot_mapping,
-                                                      const float *__restrict__ pit,
-                                                      const float *__restrict__ midpoints,
-                                                      const float *__restrict__ centroids,
-                                                      uint8_t *__restrict__ cache, int rows, int num_kv_heads,
-                                                      int block_size, int64_t block_stride,
-                                                      int norm_correction) {
+__global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4))) void store_kernel(
+    const T *__restrict__ key, const T *__restrict__ value, const int32_t *__restrict__ slot_mapping,
+    const float *__restrict__ pit, const float *__restrict__ midpoints, const float *__restrict__ centroids,
+    uint8_t *__restrict__ cache, int rows, int num_kv_heads, int block_size, int64_t block_stride,
+    int norm_correction) {
     __shared__ __align__(16) _Float16 pt_hi[kHeadDim * kHeadDim];
     __shared__ __align__(16) _Float16 pt_lo[kHeadDim * kHeadDim];
     __shared__ float c2tab[16];
+    __shared__ __align__(16) float4 btab[kCells];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int n = lane & 15, g = lane >> 4;
+    const int tiles = (rows + kRows - 1) / kRows;
+    const int stride = gridDim.x * kWaves;
+    int tile = blockIdx.x * kWaves + wave;
+
+    // the first tile's K and V loads go out before the staging below
+    constexpr bool kEarlyV = sizeof(T) < 4;
+    Chunk<T> kr, vr;
+    {
+        const int64_t row = (int64_t)tile * kRows + n;
+        load_raw(kr, key + row * kHeadDim + 32 * g, row < rows);
+        if constexpr (kEarlyV)
+            load_raw(vr, value + row * kHeadDim + 32 * g, row < rows);
+    }
+
     // thread (c, k8): 16 * PiT[8k8 .. 8k8+7][c] (coalesced over c) -> one 16-byte LDS write
     // into each part
 #pragma unroll
@@ -148,43 +170,66 @@ __global__ __launch_bounds__(kWave *kWaves) void store_kernel(const T *__restric
     }
     if (threadIdx.x < 16)
         c2tab[threadIdx.x] = norm_correction ? centroids[threadIdx.x] * centroids[threadIdx.x] : 0.f;
-    __syncthreads();
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int n = lane & 15, g = lane >> 4;
-
     float mid[15];
 #pragma unroll
     for (int i = 0; i < 15; ++i)
         mid[i] = midpoints[i];
+    float mmin = mid[0], mmax = mid[0];
+#pragma unroll
+    for (int i = 1; i < 15; ++i) {
+        mmin = fminf(mmin, mid[i]);
+        mmax = fmaxf(mmax, mid[i]);
+    }
+    const float w = (mmax - mmin) / (float)(kCells - 4);
+    const float y0 = mmin - 2.f * w;
+    int cell_ok = 1;
+    if (threadIdx.x < kCells) {
+        const int k = threadIdx.x;
+        const float lo = y0 + (float)k * w - w * (1.f / 64), hi = y0 + (float)(k + 1) * w + w * (1.f / 64);
+        int base = 0, inside = 0;
+        float m_in = __builtin_nanf("");  // compares false with every y
+#pragma unroll
+        for (int i = 0; i < 15; ++i) {
+            base += mid[i] < lo ? 1 : 0;
+            if (mid[i] >= lo && mid[i] <= hi) {
+                ++inside;
+                m_in = mid[i];
+            }
+        }
+        cell_ok = inside <= 1 && w > 0.f && w < __builtin_inff();
+        const int up = base < 15 ? base + 1 : 15;
+        // the midpoint is stored x 256, the scale of the rotation's results
+        btab[k] = float4{256.f * m_in, __builtin_bit_cast(float, base),
+                         norm_correction ? centroids[base] * centroids[base] : 0.f,
+                         norm_correction ? centroids[up] * centroids[up] : 0.f};
+    }
+    const bool use_cells = __syncthreads_and(cell_ok) != 0;
+    // cell coordinate (y - y0) / w of y = acc / 256
+    const float inv_w = (1.f / w) * (1.f / 256.f), c0 = -y0 * (1.f / w);
 
-    const int tiles = (rows + kRows - 1) / kRows;
-    for (int tile = blockIdx.x * kWaves + wave; tile < tiles; tile += gridDim.x * kWaves) {
+    for (; tile < tiles; tile += stride) {
         const int row = tile * kRows + n;
         const bool in_range = row < rows;
         const int tok = in_range ? row / num_kv_heads : 0;
         const int head = in_range ? row % num_kv_heads : 0;
+        const int64_t nrow = (int64_t)(tile + stride) * kRows + n;  // next tile of this wave
 
         // K: norm and x_hat of the lane's 32 dims
         float x[32];
-        if (in_range) {
-            load_chunk(x, key + (int64_t)row * kHeadDim + 32 * g);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i)
-                x[i] = 0.f;
-        }
+        to_floats(x, kr);
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i)
             ss = fmaf(x[i], x[i], ss);
         const float norm = sqrtf(row_sum(ss));
-        // x_hat * 16 (the division as written, then an exact power-of-two scale)
+        // x_hat * 16 (16 is an exact power-of-two scale)
+        const float rn = 16.f / (norm + 1e-8f);
         half8 b_hi[4], b_lo[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float v = 16.f * (x[8 * kb + j] / (norm + 1e-8f));
+                const float v = x[8 * kb + j] * rn;
                 b_hi[kb][j] = (_Float16)v;
                 b_lo[kb][j] = (_Float16)(v - (float)b_hi[kb][j]);
             }
@@ -208,35 +253,44 @@ __global__ __launch_bounds__(kWave *kWaves) void store_kernel(const T *__restric
                 acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, b_lo[kb], acc[cb], 0, 0, 0);
             }
         }
-        // lane (n, g): acc[cb][i] = 256 * y[row n][32g + 4cb + i]
-        float y[32];
-#pragma unroll
-        for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                y[4 * cb + i] = acc[cb][i] * (1.f / 256.f);
-        int kidx[32];
+        // lane (n, g): acc[j / 4][j % 4] = 256 * y[row n][32g + j]
+        // K indices as nibbles: element j at bits 4(j % 8) of word j / 8
+        uint32_t kw[4] = {0u, 0u, 0u, 0u};
         float csq = 0.f;
+        if (use_cells) {
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            int c = 0;
+            for (int q = 0; q < 4; ++q) {
 #pragma unroll
-            for (int i = 0; i < 15; ++i)
-                c += y[j] >= mid[i] ? 1 : 0;
-            kidx[j] = c;
-            csq += c2tab[c];
+                for (int j = 8 * q; j < 8 * q + 8; ++j) {
+                    const float a = acc[j / 4][j % 4];
+                    const float t = fminf(fmaxf(fmaf(a, inv_w, c0), 0.f), (float)(kCells - 1));
+                    const float4 e = btab[(int)t];
+                    const bool ge = a >= e.x;
+                    kw[q] |= (uint32_t)(__builtin_bit_cast(int, e.y) + (ge ? 1 : 0)) << (4 * (j % 8));
+                    csq += ge ? e.w : e.z;
+                }
+                // at most 8 table reads in flight (32 VGPRs)
+                asm volatile("" ::: "memory");
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) {
+                const float y = acc[j / 4][j % 4] * (1.f / 256.f);
+                int c = 0;
+#pragma unroll
+                for (int i = 0; i < 15; ++i)
+                    c += y >= mid[i] ? 1 : 0;
+                kw[j / 8] |= (uint32_t)c << (4 * (j % 8));
+                csq += c2tab[c];
+            }
         }
         const float csum = row_sum(csq);
         const float kscalar = norm_correction ? norm * (1.0f / sqrtf(csum + 1e-16f)) : norm;
 
         // V: per-row min / max, uniform 4-bit codes
-        if (in_range) {
-            load_chunk(x, value + (int64_t)row * kHeadDim + 32 * g);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i)
-                x[i] = 0.f;
-        }
+        if constexpr (!kEarlyV)
+            load_raw(vr, value + (int64_t)row * kHeadDim + 32 * g, in_range);
+        to_floats(x, vr);
         float lo = x[0], hi = x[0];
 #pragma unroll
         for (int i = 1; i < 32; ++i) {
@@ -246,40 +300,50 @@ __global__ __launch_bounds__(kWave *kWaves) void store_kernel(const T *__restric
         const float vmin = row_min(lo), vmax = row_max(hi);
         float scale = (vmax - vmin) / 15.0f;
         scale = scale > 1e-8f ? scale : 1e-8f;
-        int vcode[32];
+        const float rs = 1.f / scale;
+        uint32_t vw[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
-            const int c = (int)((x[j] - vmin) / scale + 0.5f);
-            vcode[j] = c < 0 ? 0 : (c > 15 ? 15 : c);
+            float f = (x[j] - vmin) * rs + 0.5f;
+            if (fabsf(f - rintf(f)) < 0x1p-16f) {  // near a code boundary: the division
+                asm volatile("");                   // (keeps it behind the branch)
+                f = (x[j] - vmin) / scale + 0.5f;
+            }
+            const int c = (int)f;
+            vw[j / 8] |= (uint32_t)(c < 0 ? 0 : (c > 15 ? 15 : c)) << (4 * (j % 8));
         }
 
         const int slot = in_range ? slot_mapping[tok] : -1;
-        if (slot < 0)
-            continue;
-        const int64_t blk = slot / block_size, off = slot % block_size;
-        uint8_t *base = cache + blk * block_stride;
-        const uint4 kb = pack32(kidx), vb = pack32(vcode);
-        if constexpr (LAYOUT == 0) {
-            uint8_t *rec = base + (off * num_kv_heads + head) * kSoaRecord;
-            *reinterpret_cast<uint4 *>(rec + 16 * g) = kb;
-            *reinterpret_cast<uint4 *>(rec + kHalfD + 16 * g) = vb;
-            if (g == 0) {
-                uint16_t *meta = reinterpret_cast<uint16_t *>(base + (int64_t)block_size * num_kv_heads * kSoaRecord) +
-                                 (int64_t)head * 3 * block_size + off;
-                meta[0] = half_bits(kscalar);
-                meta[block_size] = half_bits(scale);
-                meta[2 * block_size] = half_bits(vmin);
-            }
-        } else {
-            uint8_t *sl = base + (off * num_kv_heads + head) * kAosSlot;
-            store16_a2(sl + 16 * g, kb);
-            store16_a2(sl + kHalfD + 2 + 16 * g, vb);
-            if (g == 0) {
-                reinterpret_cast<uint16_t *>(sl + kHalfD)[0] = half_bits(kscalar);
-                reinterpret_cast<uint16_t *>(sl + kHeadDim + 2)[0] = half_bits(scale);
-                reinterpret_cast<uint16_t *>(sl + kHeadDim + 4)[0] = half_bits(vmin);
+        if (slot >= 0) {
+            const int64_t blk = slot / block_size, off = slot % block_size;
+            uint8_t *base = cache + blk * block_stride;
+            const uint4 kb = uint4{kw[0], kw[1], kw[2], kw[3]}, vb = uint4{vw[0], vw[1], vw[2], vw[3]};
+            if constexpr (LAYOUT == 0) {
+                uint8_t *rec = base + (off * num_kv_heads + head) * kSoaRecord;
+                *reinterpret_cast<uint4 *>(rec + 16 * g) = kb;
+                *reinterpret_cast<uint4 *>(rec + kHalfD + 16 * g) = vb;
+                if (g == 0) {
+                    uint16_t *meta = reinterpret_cast<uint16_t *>(base + (int64_t)block_size * num_kv_heads * kSoaRecord) +
+                                     (int64_t)head * 3 * block_size + off;
+                    meta[0] = half_bits(kscalar);
+                    meta[block_size] = half_bits(scale);
+                    meta[2 * block_size] = half_bits(vmin);
+                }
+            } else {
+                uint8_t *sl = base + (off * num_kv_heads + head) * kAosSlot;
+                store16_a2(sl + 16 * g, kb);
+                store16_a2(sl + kHalfD + 2 + 16 * g, vb);
+                if (g == 0) {
+                    reinterpret_cast<uint16_t *>(sl + kHalfD)[0] = half_bits(kscalar);
+                    reinterpret_cast<uint16_t *>(sl + kHeadDim + 2)[0] = half_bits(scale);
+                    reinterpret_cast<uint16_t *>(sl + kHeadDim + 4)[0] = half_bits(vmin);
+                }
             }
         }
+        // the next tile of this wave
+        load_raw(kr, key + nrow * kHeadDim + 32 * g, nrow < rows);
+        if constexpr (kEarlyV)
+            load_raw(vr, value + nrow * kHeadDim + 32 * g, nrow < rows);
     }
 }
 

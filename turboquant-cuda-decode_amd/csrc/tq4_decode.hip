@@ -388,6 +388,9 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
                     block_size, Hk, (long long)cache_block_stride);
     if (!aligned(key, 16) || !aligned(value, 16) || !aligned(kv_cache, 16))
         return fail(TQ4_E_INVALID, "tq4_store: key, value and kv_cache must be 16-byte aligned");
+    if ((int64_t)N * Hk > INT32_MAX - 64)
+        return fail(TQ4_E_INVALID, "tq4_store: N * Hk = %lld rows exceeds the 32-bit row index",
+                    (long long)N * Hk);
     if (N == 0)
         return ok();
     const int rows = N * Hk;
