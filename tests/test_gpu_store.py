@@ -198,3 +198,30 @@ def test_reference_store_signature_and_skipped_slots(dev):
     with pytest.raises(RuntimeError):
         ops.triton_turboquant_store(t(key).half(), t(value).half(), cache, t(slots), t(rot_t), t(mids),
                                     mse_bits=3, key_packed_size=66, value_quant_bits=4)
+
+
+def test_reference_module_names(dev):
+    """``tq4_decode.soa_store`` / ``tq4_decode.aos_store`` expose ``triton_turboquant_store``
+    with the reference modules' signatures and write what ``ops.store`` writes."""
+    from tq4_decode import aos_store, soa_store
+
+    key, value, slots, rot_t, cents, mids = make_inputs(17, 64, 8, "bf16")
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    k, v = t(key).bfloat16(), t(value).bfloat16()
+    for mod, layout, nc in ((soa_store, "soa", True), (aos_store, "aos", False)):
+        a = torch.zeros(8, BS, HK, 134, dtype=torch.uint8, device=dev)
+        b = torch.zeros_like(a)
+        kwargs = dict(centroids=t(cents), norm_correction=nc) if layout == "soa" else {}
+        mod.triton_turboquant_store(k, v, a, t(slots), t(rot_t), t(mids), mse_bits=4,
+                                    key_packed_size=66, value_quant_bits=4, **kwargs)
+        ops.store(k, v, b, t(slots), t(rot_t), t(mids), t(cents), layout=layout, norm_correction=nc)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), layout
+        ref = ostore.store(key, value, slots, rot_t, cents, np.zeros((8, BS, HK, 134), np.uint8),
+                           block_size=BS, is_aos=layout == "aos")
+        keep = np.nonzero(slots >= 0)[0]
+        gather = OL.gather_aos if layout == "aos" else OL.gather_soa
+        for h in range(HK):
+            gv = gather(a.cpu().numpy(), slots[keep] // BS, slots[keep] % BS, h, BS, HK, D)[2]
+            rv = gather(ref, slots[keep] // BS, slots[keep] % BS, h, BS, HK, D)[2]
+            assert np.array_equal(gv, rv)

@@ -273,6 +273,18 @@ def triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, 
           norm_correction=norm_correction)
 
 
+def aos_triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits,
+                                key_packed_size, value_quant_bits, key_fp8=False):
+    """AoS cache writer with the ``reference/aos_store.py:350-361`` signature (MSE path,
+    4-bit keys and values; the slot keeps the raw fp16 norm, no norm correction)."""
+    if key_fp8:
+        raise NotImplementedError("FP8 keys (the k8v4 presets) are not built")
+    _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
+    _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
+    store(key, value, kv_cache, slot_mapping, PiT, midpoints, None, layout="aos",
+          norm_correction=False)
+
+
 class _CudaExtCompat:
     """Methods named like the reference CUDA extension modules (``cuda/tq4_cuda_v*_bind.cpp``).
 
