@@ -68,9 +68,11 @@ def traffic_from_profile(name: str):
 
 
 class HipEvents:
-    """HIP events recorded on the launch stream, created without the system-scope release
-    fence (hipEventDisableSystemFence), so the interval covers the kernel and not an L2
-    write-back of its output; these intervals match rocprofv3's kernel durations."""
+    """HIP events on the launch stream, created without the system-scope release fence
+    (hipEventDisableSystemFence).  Two ways to take an interval: record a pair around a
+    launch (includes the dispatch of the kernel and of the second marker), or hand a pair
+    to the library's next kernel launch (``tq4_time_next_launch``: hipExtLaunchKernel
+    stamps them with the kernel's own start and end, the duration rocprofv3 reports)."""
 
     NO_SYSTEM_FENCE = 0x20000000
 
@@ -103,6 +105,12 @@ class HipEvents:
         if self.hip.hipEventRecord(e, self.stream) != 0:
             raise RuntimeError("hipEventRecord failed")
 
+    def stamp_next_launch(self, a, b):
+        from tq4_decode import _lib
+
+        if _lib.load().tq4_time_next_launch(a, b) != 0:
+            raise RuntimeError("tq4_time_next_launch failed")
+
     def elapsed_ms(self, a, b) -> float:
         ms = self.ct.c_float()
         if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
@@ -115,8 +123,8 @@ class HipEvents:
 
 
 def store_times(dev, flush, timer, reps=30):
-    """Cache writer (tq4_store, SoA, bf16 K/V, norm correction) cold: one decode step
-    (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  Bytes per (token,
+    """Cache writer (tq4_store, SoA, bf16 K/V, norm correction) cold, kernel duration: one
+    decode step (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  Bytes per (token,
     kv-head): 2 x 256 read + 134 written, plus 4 of slot mapping per token."""
     import numpy as np
     import torch
@@ -139,9 +147,8 @@ def store_times(dev, flush, timer, reps=30):
         for i in range(reps + 3):
             flush.sum()
             a, b = timer.pair()
-            timer.record(a)
+            timer.stamp_next_launch(a, b)  # the kernel's own start and end
             ops.store(key, val, cache, slots, rot, m, c)
-            timer.record(b)
             torch.cuda.synchronize()
             if i >= 3:
                 times.append(timer.elapsed_ms(a, b) * 1e3)
@@ -242,7 +249,9 @@ def main() -> int:
 
     timer = HipEvents(torch.cuda.current_stream(dev).cuda_stream)
 
-    def cold_times(layout, kernel, steps, warmup):
+    def cold_times(layout, kernel, steps, warmup, stamped=True):
+        """Durations (ms) of `steps` cold launches: the kernel's own start/end stamps, or
+        (stamped=False) events recorded around each launch."""
         for _ in range(warmup):
             flush.sum()
             launch(layout, kernel)
@@ -250,13 +259,17 @@ def main() -> int:
         ev = [timer.pair() for _ in range(steps)]
         for a, b in ev:
             flush.sum()  # 1 GiB read sweep: evicts L2 and the Infinity Cache
-            timer.record(a)
-            launch(layout, kernel)
-            timer.record(b)
+            if stamped:
+                timer.stamp_next_launch(a, b)
+                launch(layout, kernel)
+            else:
+                timer.record(a)
+                launch(layout, kernel)
+                timer.record(b)
         torch.cuda.synchronize()
         out = [timer.elapsed_ms(a, b) for a, b in ev]
-        for a, b in ev:
-            timer.destroy(a, b)
+        for e in ev:
+            timer.destroy(*e)
         return out
 
     def warm_time(layout, kernel, iters=100, rounds=5):
@@ -276,6 +289,7 @@ def main() -> int:
 
     torch.cuda.synchronize()
     ms = cold_times(args.layout, args.kernel, args.steps, args.warmup)
+    around = cold_times(args.layout, args.kernel, 50, 2, stamped=False)
     mean_ms = statistics.fmean(ms)
     med_ms = statistics.median(ms)
     gbs = nbytes / (mean_ms * 1e-3) / 1e9
@@ -302,6 +316,10 @@ def main() -> int:
                    "cache": "cold (1 GiB sweep)"},
         "stage1_us": round(mean_ms * 1e3, 2),
         "stage1_us_median": round(med_ms * 1e3, 2),
+        "stage1_us_with_dispatch": round(statistics.fmean(around) * 1e3, 2),
+        "timing": "kernel start/end stamped by hipExtLaunchKernel events (the interval "
+                  "rocprofv3 reports); stage1_us_with_dispatch: mean of 50 further cold "
+                  "launches timed by events recorded around each launch",
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "algorithmic_bytes": nbytes,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,

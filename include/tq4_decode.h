@@ -131,6 +131,15 @@ const char *tq4_last_error(void);
 /* ABI version of this library (major*100 + minor). */
 int tq4_abi_version(void);
 
+/*
+ * Measurement hook: the next kernel launch made by this thread stamps start_event and
+ * stop_event (hipEvent_t, created by the caller; either may be NULL) with that kernel's
+ * own start and end (hipExtLaunchKernel), the interval rocprofv3 reports as its
+ * duration; the hook then clears itself.  An entry point that launches several kernels
+ * (tq4_full_decode) stamps the first.  No counterpart in the reference: for benchmarks.
+ */
+int tq4_time_next_launch(void *start_event, void *stop_event);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,7 @@
 // baseline/triton_v2.py:594-607, but report through a return code and a thread-local
 // message instead of throwing.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstdlib>
 
 #include <cstdarg>
@@ -21,6 +22,24 @@
 namespace {
 
 thread_local char g_err[512] = "";
+
+// Events the next kernel launch of this thread stamps with its own start and end
+// (tq4_time_next_launch); cleared by that launch.
+thread_local hipEvent_t g_time_start = nullptr, g_time_stop = nullptr;
+
+// Every kernel launch goes through here: arguments are converted to the kernel's
+// parameter types (the event-stamping launch passes them by address).
+template <typename... KArgs, typename... Args>
+void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t st, Args... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "argument count");
+    if (g_time_start || g_time_stop) {
+        const hipEvent_t a = g_time_start, b = g_time_stop;
+        g_time_start = g_time_stop = nullptr;
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, st, a, b, 0, static_cast<KArgs>(args)...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, 0, st, static_cast<KArgs>(args)...);
+    }
+}
 
 int fail(int code, const char *fmt, ...) {
     va_list ap;
@@ -89,7 +108,7 @@ int check_stage1(const Stage1Args &a) {
 
 template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t st) {
     const dim3 grid(a.S, a.Hk, a.B);
-    hipLaunchKernelGGL((tq4::stage1_simple_kernel<LAYOUT, G>), grid, dim3(tq4::kWave), 0, st,
+    launch(&tq4::stage1_simple_kernel<LAYOUT, G>, grid, dim3(tq4::kWave), st,
                        a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk, a.bs,
                        a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
@@ -137,7 +156,7 @@ template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_
                                               &tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>),
                                        slots),
                     a.B);
-    hipLaunchKernelGGL((tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>), grid, dim3(tq4::kWave), 0, st,
+    launch(&tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>, grid, dim3(tq4::kWave), st,
                        a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk,
                        log2_int(a.bs), a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
@@ -160,7 +179,7 @@ template <int LAYOUT, int G> int xdl_waves(const Stage1Args &a) {
 template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
     const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>()>;
     const dim3 grid(a.Hk, xdl_waves<LAYOUT, G>(a), a.B);
-    hipLaunchKernelGGL(kernel, grid, dim3(tq4::kWave), 0, st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
+    launch(kernel, grid, dim3(tq4::kWave), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
                        a.mid_o, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks, a.stride, a.S,
                        a.scale * tq4::kLog2e);
 }
@@ -247,15 +266,15 @@ int rotate_query(const void *query, int query_dtype, const float *rot_t, float *
     const dim3 grid((rows + tq4::kRotMfmaRows - 1) / tq4::kRotMfmaRows), block(tq4::kWave * tq4::kRotWaves);
     switch (query_dtype) {
     case TQ4_F32:
-        hipLaunchKernelGGL(tq4::rotate_mfma_kernel<float>, grid, block, 0, st,
+        launch(&tq4::rotate_mfma_kernel<float>, grid, block, st,
                            static_cast<const float *>(query), rot_t, q_rot, rows, centroids, pair_lut);
         break;
     case TQ4_BF16:
-        hipLaunchKernelGGL(tq4::rotate_mfma_kernel<__bf16>, grid, block, 0, st,
+        launch(&tq4::rotate_mfma_kernel<__bf16>, grid, block, st,
                            static_cast<const __bf16 *>(query), rot_t, q_rot, rows, centroids, pair_lut);
         break;
     case TQ4_F16:
-        hipLaunchKernelGGL(tq4::rotate_mfma_kernel<_Float16>, grid, block, 0, st,
+        launch(&tq4::rotate_mfma_kernel<_Float16>, grid, block, st,
                            static_cast<const _Float16 *>(query), rot_t, q_rot, rows, centroids, pair_lut);
         break;
     default:
@@ -267,6 +286,12 @@ int rotate_query(const void *query, int query_dtype, const float *rot_t, float *
 }  // namespace
 
 extern "C" {
+
+int tq4_time_next_launch(void *start_event, void *stop_event) {
+    g_time_start = reinterpret_cast<hipEvent_t>(start_event);
+    g_time_stop = reinterpret_cast<hipEvent_t>(stop_event);
+    return ok();
+}
 
 int tq4_abi_version(void) { return 100; }
 
@@ -305,15 +330,15 @@ int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_d
     const dim3 grid(Hq, B);
     switch (out_dtype) {
     case TQ4_F32:
-        hipLaunchKernelGGL(tq4::stage2_kernel<float>, grid, dim3(tq4::kWave), 0, st, mid_o,
+        launch(&tq4::stage2_kernel<float>, grid, dim3(tq4::kWave), st, mid_o,
                            seq_lens, static_cast<float *>(out), lse, Hq, num_kv_splits);
         break;
     case TQ4_BF16:
-        hipLaunchKernelGGL(tq4::stage2_kernel<__bf16>, grid, dim3(tq4::kWave), 0, st, mid_o,
+        launch(&tq4::stage2_kernel<__bf16>, grid, dim3(tq4::kWave), st, mid_o,
                            seq_lens, static_cast<__bf16 *>(out), lse, Hq, num_kv_splits);
         break;
     case TQ4_F16:
-        hipLaunchKernelGGL(tq4::stage2_kernel<_Float16>, grid, dim3(tq4::kWave), 0, st, mid_o,
+        launch(&tq4::stage2_kernel<_Float16>, grid, dim3(tq4::kWave), st, mid_o,
                            seq_lens, static_cast<_Float16 *>(out), lse, Hq, num_kv_splits);
         break;
     default:
@@ -335,8 +360,8 @@ int tq4_build_pair_lut(const float *centroids, float *pair_lut, int n_centroids,
     if (n_centroids != 16)
         return fail(TQ4_E_UNSUPPORTED, "tq4_build_pair_lut: 16 centroids (4-bit keys) expected, got %d",
                     n_centroids);
-    hipLaunchKernelGGL(tq4::pair_lut_kernel, dim3(1), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), centroids, pair_lut, n_centroids);
+    launch(&tq4::pair_lut_kernel, dim3(1), dim3(256), reinterpret_cast<hipStream_t>(stream), centroids,
+           pair_lut, n_centroids);
     return launch_status("pair_lut");
 }
 
@@ -398,10 +423,9 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
     const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, tq4::store::kMaxGroups));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define TQ4_STORE_LAUNCH(L, T)                                                                       \
-    hipLaunchKernelGGL((tq4::store::store_kernel<L, T>), grid, dim3(tq4::kWave * tq4::store::kWaves), 0, st, \
-                       static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, \
-                       midpoints, centroids, kv_cache, rows, Hk, block_size, cache_block_stride,       \
-                       norm_correction)
+    launch(&tq4::store::store_kernel<L, T>, grid, dim3(tq4::kWave * tq4::store::kWaves), st,         \
+           static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, midpoints, \
+           centroids, kv_cache, rows, Hk, block_size, cache_block_stride, norm_correction)
     switch (dtype * 2 + layout) {
     case TQ4_F32 * 2 + 0: TQ4_STORE_LAUNCH(0, float); break;
     case TQ4_F32 * 2 + 1: TQ4_STORE_LAUNCH(1, float); break;

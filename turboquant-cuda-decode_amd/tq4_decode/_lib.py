@@ -26,6 +26,7 @@ EXPORTS = (
     "tq4_store",
     "tq4_last_error",
     "tq4_abi_version",
+    "tq4_time_next_launch",
 )
 
 _handle = None
@@ -42,6 +43,7 @@ _SIGS = {
     "tq4_store": [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _p],
     "tq4_last_error": [],
     "tq4_abi_version": [],
+    "tq4_time_next_launch": [_p, _p],
 }
 
 
