@@ -636,9 +636,25 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     constexpr int TPL = G / 4;
     constexpr int RING = 4;
     const int block_size = 1 << block_size_log2;
-    const int kvh = blockIdx.x;
-    const int wid = blockIdx.y, nw = gridDim.y;
-    const int b = blockIdx.z;
+    int kvh = blockIdx.x, wid = blockIdx.y, b = blockIdx.z;
+    const int nw = gridDim.y;
+    if constexpr (LAYOUT == 1) {
+        // Workgroups are dealt to the XCDs round-robin by linear id (8 on gfx950), so with
+        // the plain map kv-head h runs on XCD h.  An AoS slot of kv-head h shares 128-byte
+        // lines with the slots of h - 1 and h + 1: the kv-heads of one (sequence, wave)
+        // pair go to one XCD instead, so each line is fetched from HBM into one L2 (halves
+        // the HBM reads).  A bijection of the grid whenever the pair count is a multiple of 8.
+        constexpr int kXcds = 8;
+        const int hk = gridDim.x, pairs = gridDim.y * gridDim.z;
+        if (pairs % kXcds == 0) {
+            const int lin = blockIdx.x + hk * (blockIdx.y + gridDim.y * blockIdx.z);
+            const int r = lin / kXcds;
+            const int pair = lin % kXcds + kXcds * (r / hk);
+            kvh = r % hk;
+            wid = pair % nw;
+            b = pair / nw;
+        }
+    }
     const int lane = threadIdx.x;
     // The pair-LUT rows and q do not depend on the sequence length: they go out first, the
     // K table and the q operands are built once the first tiles' loads are on their way.
