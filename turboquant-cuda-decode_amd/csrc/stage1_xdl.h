@@ -148,7 +148,6 @@ struct LaneOffsets {
     uint32_t m;      // SoA: norm of the lane's first softmax token within its field array; AoS: its slot
     int tok_stride;  // bytes between consecutive tokens of one kv-head
     int mf;          // SoA: bytes between the three metadata arrays
-    int v_shift;     // AoS: v0 & 3 (the same in every lane)
 };
 
 template <int LAYOUT, int G>
@@ -166,11 +165,9 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int h
     if (LAYOUT == 0) {
         o.m = (kvh * 3 * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
         o.mf = block_size * 2;
-        o.v_shift = 0;
     } else {
         o.m = (st * hk + kvh) * kAosSlot;
         o.mf = 0;
-        o.v_shift = (kvh * kAosSlot + kHalfD + 2) & 3;  // lane terms are multiples of 4
     }
     return o;
 }
@@ -178,33 +175,24 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int h
 // Raw K loads of one tile.
 template <int LAYOUT> struct RawK;
 template <> struct RawK<0> { uint4 k; };
-template <> struct RawK<1> { uint32_t k[5]; };  // aligned dwords around the 2-byte aligned bytes
+template <> struct RawK<1> { uint4 k; };  // 2-byte aligned: gfx950 buffer loads take any byte offset
 // Raw V + metadata loads of one tile.  SoA metadata of two consecutive tokens comes in
-// one dword (TPL = 2); AoS metadata in one 16-bit load per token and field.
+// one dword (TPL = 2); AoS: the norm in a 16-bit load per token, the adjacent scale and
+// zero in one dword per token.
 template <int LAYOUT, int TPL> struct RawV;
 template <int TPL> struct RawV<0, TPL> {
     uint32_t v[4];
     uint32_t norm, scale, zero;
 };
 template <int TPL> struct RawV<1, TPL> {
-    uint2 v[4];  // aligned dword pairs around each V dword
-    uint32_t norm[TPL], scale[TPL], zero[TPL];
+    uint32_t v[4];
+    uint32_t norm[TPL], scale_zero[TPL];
 };
 
 template <int LAYOUT>
 __device__ __forceinline__ void issue_k(RawK<LAYOUT> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
                                         const LaneOffsets &o) {
-    if constexpr (LAYOUT == 0) {
-        t.k = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
-    } else {
-        const uint32_t ka = o.k & ~3u;
-        const auto k03 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, ka, doff, 0);
-        t.k[0] = k03[0];
-        t.k[1] = k03[1];
-        t.k[2] = k03[2];
-        t.k[3] = k03[3];
-        t.k[4] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, ka + 16, doff, 0);
-    }
+    t.k = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
 }
 
 template <int LAYOUT, int TPL>
@@ -224,20 +212,13 @@ __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rs
             t.zero = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m, moff + 2 * o.mf, 0);
         }
     } else {
-        // token 4g+i's V dword starts sh = (v_shift + i * tok_stride) & 3 bytes past a
-        // dword; both offsets below are multiples of 4 and non-negative.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int sh = (o.v_shift + i * o.tok_stride) & 3;
-            t.v[i] = __builtin_bit_cast(
-                uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                           rsrc, o.v0 - o.v_shift, doff + i * o.tok_stride + o.v_shift - sh, 0));
-        }
+        for (int i = 0; i < 4; ++i)
+            t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
 #pragma unroll
         for (int j = 0; j < TPL; ++j) {
             t.norm[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHalfD, doff + j * o.tok_stride, 0);
-            t.scale[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHeadDim + 2, doff + j * o.tok_stride, 0);
-            t.zero[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHeadDim + 4, doff + j * o.tok_stride, 0);
+            t.scale_zero[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m + kHeadDim + 2, doff + j * o.tok_stride, 0);
         }
     }
 }
@@ -245,14 +226,7 @@ __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rs
 // The K bytes of lane (n, g) (token n, bytes 16g ..), gathered from the loading lanes.
 template <int LAYOUT>
 __device__ __forceinline__ uint4 decode_k(const RawK<LAYOUT> &t, const LaneOffsets &o) {
-    uint4 w;
-    if constexpr (LAYOUT == 0) {
-        w = t.k;
-    } else {
-        const uint32_t sh = o.k & 3u;
-        w = uint4{__builtin_amdgcn_alignbyte(t.k[1], t.k[0], sh), __builtin_amdgcn_alignbyte(t.k[2], t.k[1], sh),
-                  __builtin_amdgcn_alignbyte(t.k[3], t.k[2], sh), __builtin_amdgcn_alignbyte(t.k[4], t.k[3], sh)};
-    }
+    const uint4 w = t.k;
     return uint4{(uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.x),
                  (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.y),
                  (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.z),
@@ -278,15 +252,15 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            r.v[i] = __builtin_amdgcn_alignbyte(t.v[i].y, t.v[i].x, (o.v_shift + i * o.tok_stride) & 3);
+            r.v[i] = t.v[i];
         if constexpr (TPL == 1) {
             r.norm = t.norm[0];
-            r.scale = t.scale[0];
-            r.zero = t.zero[0];
+            r.scale = t.scale_zero[0] & 0xFFFFu;
+            r.zero = t.scale_zero[0] >> 16;
         } else {
             r.norm = (t.norm[0] & 0xFFFFu) | (t.norm[1] << 16);
-            r.scale = (t.scale[0] & 0xFFFFu) | (t.scale[1] << 16);
-            r.zero = (t.zero[0] & 0xFFFFu) | (t.zero[1] << 16);
+            r.scale = __builtin_amdgcn_perm(t.scale_zero[1], t.scale_zero[0], 0x05040100u);
+            r.zero = __builtin_amdgcn_perm(t.scale_zero[1], t.scale_zero[0], 0x07060302u);
         }
     }
     return r;
