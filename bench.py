@@ -193,6 +193,34 @@ def full_decode_time(dev, flush, timer, reps=30):
 
 
 def cpu_baseline(w, threads: int, repeats: int = 3):
+    """The reference's fp32 Stage1 math in PyTorch on the host cores (the oracle's
+    vectorized restatement of tools/cuda_v1_diagnostic.py:106-224), whole workload."""
+    import torch
+
+    from oracle import torch_stage1
+
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    times = []
+    try:
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            torch_stage1.stage1(w.q_rot, w.kv_cache, w.block_table, w.seq_lens, w.centroids,
+                                w.num_kv_splits, num_kv_heads=w.num_kv_heads)
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    t = statistics.median(times)
+    return {"value": round(algorithmic_bytes(w) / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "seconds": round(t, 4),
+            "sample": (f"whole workload ({w.batch} seqs x {int(w.seq_lens[0])} tokens, SoA): the "
+                       f"reference's fp32 Stage1 math in PyTorch on the CPU (oracle/torch_stage1.py, "
+                       f"restating tools/cuda_v1_diagnostic.py:106-224), {threads} torch threads, "
+                       f"median of {repeats}")}
+
+
+def cpu_baseline_c(w, threads: int, repeats: int = 3):
+    """The C oracle (Triton V1 program restated, fp32, OpenMP) over the whole workload."""
     from oracle import native
 
     native.lib()
@@ -205,9 +233,7 @@ def cpu_baseline(w, threads: int, repeats: int = 3):
     t = statistics.median(times)
     return {"value": round(algorithmic_bytes(w) / t / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port", "seconds": round(t, 4),
-            "sample": (f"whole workload ({w.batch} seqs x {int(w.seq_lens[0])} tokens, SoA), "
-                       f"C oracle tq4o_stage1 (Triton V1 program restated, fp32, OpenMP), "
-                       f"median of {repeats}")}
+            "sample": "whole workload, C oracle tq4o_stage1 (OpenMP), median of %d" % repeats}
 
 
 def main() -> int:
@@ -350,6 +376,7 @@ def main() -> int:
         except AttributeError:
             threads = min(16, os.cpu_count() or 1)
         result["cpu_baseline"] = cpu_baseline(w, threads)
+        result["cpu_baseline_c"] = cpu_baseline_c(w, threads)
     print(json.dumps(result))
     return 0
 

@@ -19,8 +19,10 @@ Contents (each function cites the reference ``file:line`` it restates):
                  ``:223-373``, ``:482-485``; ``reference/aos_store.py:317-325``).
 * ``tq4_oracle.c`` + ``native``  a plain-C float32 restatement of the Triton V1
                  Stage1 programs (one program per (batch, q-head, split), BLOCK_KV=4
-                 online softmax) and of Stage2; it is the full-size checker and the
-                 CPU baseline.
+                 online softmax) and of Stage2; it is the full-size checker.
+* ``torch_stage1`` the reference's fp32 Stage1 math in PyTorch on the CPU
+                 (``tools/cuda_v1_diagnostic.py:106-224``), vectorized over the heads
+                 and splits of a sequence; the CPU baseline of ``bench.py``.
 
 Pins (what checks each function against something other than itself) live in
 ``tests/test_oracle_*.py``.  Parity status per function is listed in the module

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import layout, native, stage1
+from oracle import layout, native, stage1, torch_stage1
 from tq4_decode import workloads
 
 
@@ -69,6 +69,36 @@ def test_c_oracle_matches_numpy_oracle(hq, hk, lens, splits, is_aos):
     o, l = stage1.stage2(ref, w.seq_lens)
     co, cl = native.stage2(got, w.seq_lens)
     assert np.abs(o - co).max() < 2e-6 and np.abs(l - cl).max() < 2e-6
+
+
+@pytest.mark.parametrize("hq,hk,lens,splits", [
+    (32, 8, [1, 17, 256, 300], 4),
+    (32, 8, [512, 33, 0], 32),
+    (64, 8, [700], 16),
+    (8, 8, [90, 3], 8),
+    (16, 4, [45, 1000], 5),
+])
+@pytest.mark.parametrize("is_aos", [False, True])
+def test_torch_cpu_restatement_matches_numpy_oracle(hq, hk, lens, splits, is_aos):
+    """The vectorized torch fp32 restatement (the CPU baseline) against the float64 oracle,
+    including an empty sequence and empty splits."""
+    w = _small(23, lens, splits, hq, hk)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, hk) if is_aos else w.kv_cache
+    ref = stage1.stage1(w.q_rot, cache, w.block_table, w.seq_lens, w.centroids, splits,
+                        num_kv_heads=hk, is_aos=is_aos)
+    got = torch_stage1.stage1(w.q_rot, cache, w.block_table, w.seq_lens, w.centroids, splits,
+                              num_kv_heads=hk, is_aos=is_aos)
+    assert np.array_equal(np.isnan(ref), np.isnan(got))
+    assert np.nanmax(np.abs(ref - got)) < 2e-6
+
+
+def test_torch_cpu_restatement_matches_config1_fixture(config1):
+    f = config1
+    for lay, aos in (("soa", False), ("aos", True)):
+        got = torch_stage1.stage1(f["q_rot"], f[f"cache_{lay}"], f["block_table"], f["seq_lens"],
+                                  f["centroids"], int(f["num_kv_splits"]),
+                                  num_kv_heads=int(f["num_kv_heads"]), is_aos=aos)
+        assert np.nanmax(np.abs(got - f[f"mid_{lay}"])) < 2e-6
 
 
 @pytest.mark.parametrize("splits", [1, 3, 4, 16, 32, 64])
