@@ -102,3 +102,45 @@ def test_full_decode_reference_ext_shape(dev):
                                         w.centroids, num_kv_heads=8)
     assert np.abs(out.cpu().numpy() - fo).max() <= 1e-4
     assert np.abs(lse.cpu().numpy() - fl).max() <= 1e-4
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_backend_decode_entry(dev, layout):
+    """``tq4_decode.{soa,aos}_decode.triton_turboquant_decode_attention`` with the backend's
+    arguments (Pi, not PiT; workspace buffers; fixed split count) against the oracle."""
+    from tq4_decode import aos_decode, soa_decode
+
+    rng = np.random.default_rng(206)
+    w = workloads.small(206, 5, [1500, 1, 333, 4096, 64], 32)
+    query = rng.standard_normal((5, 32, 128)).astype(np.float16)
+    rot_t = workloads.random_orthogonal(rng, 128)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, 8) if layout == "aos" else w.kv_cache
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    mid_buf = torch.empty(8, 32, 32, 129, device=dev)
+    out_buf = torch.empty(8, 32, 128, dtype=torch.float16, device=dev)
+    lse_buf = torch.empty(8, 32, device=dev)
+
+    class Holder:
+        pass
+
+    mod = aos_decode if layout == "aos" else soa_decode
+    out = mod.triton_turboquant_decode_attention(
+        t(query), t(cache), t(w.block_table), t(w.seq_lens), t(rot_t.T.copy()), t(w.centroids),
+        128 ** -0.5, mse_bits=4, key_packed_size=66, value_quant_bits=4, norm_correction=True,
+        mid_o_buf=mid_buf, output_buf=out_buf, lse_buf=lse_buf, buf_holder=Holder(),
+        max_num_kv_splits=32)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16 and out.data_ptr() == out_buf.data_ptr()
+    q_rot = (query.astype(np.float64) @ rot_t.astype(np.float64)).astype(np.float32)
+    mid = native.stage1(q_rot, cache, w.block_table, w.seq_lens, w.centroids, 32, num_kv_heads=8,
+                        is_aos=layout == "aos")
+    ro, rl = native.stage2(mid, w.seq_lens)
+    live = w.seq_lens > 0
+    err = np.abs(out.float().cpu().numpy()[live] - ro[live]).max()
+    print(f"{layout} decode entry fp16 max-abs {err:.3e}")
+    assert err <= 1e-3
+    assert np.abs(lse_buf[:5].cpu().numpy()[live] - rl[live]).max() <= 1e-4
+    with pytest.raises(NotImplementedError):
+        mod.triton_turboquant_decode_attention(
+            t(query), t(cache), t(w.block_table), t(w.seq_lens), t(rot_t.T.copy()), t(w.centroids),
+            128 ** -0.5, mse_bits=4, key_packed_size=66, value_quant_bits=4, key_fp8=True)

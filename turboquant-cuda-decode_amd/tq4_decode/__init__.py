@@ -10,7 +10,7 @@ __all__ = [
     "codebook", "layout", "workloads", "ops", "stage1", "stage2", "full_decode",
     "rotate_query", "pair_lut_device", "launch_tq4_v2_stage1", "launch_soa_v1_stage1",
     "launch_aos_v1_stage1", "launch_stage2", "ext", "DecodeWorkspace", "Tq4Error", "store",
-    "triton_turboquant_store", "aos_triton_turboquant_store",
+    "triton_turboquant_store", "aos_triton_turboquant_store", "turboquant_decode_attention",
 ]
 
 

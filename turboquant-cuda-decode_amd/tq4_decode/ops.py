@@ -232,6 +232,72 @@ def full_decode(query, rotation_t, kv_cache, block_table, seq_lens, centroids, n
     return ws.out, ws.lse
 
 
+def _buffer_view(buf, shape, dtype):
+    """``buf`` cut to ``shape`` (leading sub-block) when it fits and stays contiguous."""
+    if buf is None or buf.dtype != dtype or buf.dim() != len(shape):
+        return None
+    if any(have < want for have, want in zip(buf.shape, shape)):
+        return None
+    view = buf[tuple(slice(0, n) for n in shape)]
+    return view if view.is_contiguous() else None
+
+
+def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, centroids, scale,
+                                mse_bits, key_packed_size, value_quant_bits, key_fp8=False,
+                                norm_correction=False, PiT=None, mid_o_buf=None, output_buf=None,
+                                lse_buf=None, buf_holder=None, max_num_kv_splits=32, sinks=None, *,
+                                layout="soa"):
+    """The decode entry of the vLLM backend (``reference/soa_decode_v1.py:485-643``; AoS
+    ``reference/aos_decode.py:486-626``): ``q_rot = query @ PiT``, pair LUT, Stage1 over
+    ``max_num_kv_splits`` splits, Stage2; returns ``[B, Hq, D]`` in the query dtype.
+
+    Caller buffers are used when they fit (``mid_o_buf`` fp32 ``[>=B, Hq, S, D+1]``,
+    ``output_buf`` ``[>=B, Hq, D]`` in the query dtype, ``lse_buf`` fp32 ``[>=B, Hq]``); the
+    rotated query and the pair LUT live on ``buf_holder`` when one is given.  Built for the
+    4-bit ``turboquant_4bit_nc`` cache: FP8 keys, other bit widths, sinks and AoS without
+    norm correction raise ``NotImplementedError``.
+    """
+    if key_fp8:
+        raise NotImplementedError("FP8 keys (the k8v4 presets) are not built")
+    if sinks is not None:
+        raise NotImplementedError("attention sinks are not built")
+    _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
+    _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
+    if layout == "aos" and not norm_correction:
+        raise NotImplementedError("AoS decode is built with the norm correction (turboquant_4bit_nc)")
+    _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
+    B, Hq, D = query.shape
+    S = int(max_num_kv_splits)
+    if PiT is None:
+        PiT = Pi.t().contiguous()
+    dev = query.device
+
+    def held(name, shape, dtype):
+        buf = getattr(buf_holder, name, None) if buf_holder is not None else None
+        view = _buffer_view(buf, shape, dtype)
+        if view is None:
+            view = torch.empty(shape, dtype=dtype, device=dev)
+            if buf_holder is not None:
+                setattr(buf_holder, name, view)
+        return view
+
+    ws = DecodeWorkspace.__new__(DecodeWorkspace)
+    ws.q_rot = held("_tq4_q_rot_buf", (B, Hq, D), torch.float32)
+    ws.pair_lut = held("_tq4_pair_lut_buf", (256, 2), torch.float32)
+    ws.mid_o = _buffer_view(mid_o_buf, (B, Hq, S, D + 1), torch.float32)
+    if ws.mid_o is None:
+        ws.mid_o = held("_tq_mid_o_buf", (B, Hq, S, D + 1), torch.float32)
+    ws.out = _buffer_view(output_buf, (B, Hq, D), query.dtype)
+    if ws.out is None:
+        ws.out = held("_tq_output_buf", (B, Hq, D), query.dtype)
+    ws.lse = _buffer_view(lse_buf, (B, Hq), torch.float32)
+    if ws.lse is None:
+        ws.lse = held("_tq_lse_buf", (B, Hq), torch.float32)
+    out, _ = full_decode(query.contiguous(), PiT, kv_cache, block_table, seq_lens, centroids, S,
+                         layout=layout, out_dtype=query.dtype, attn_scale=scale, workspace=ws)
+    return out
+
+
 # ---- reference harness call shapes -------------------------------------------------
 
 def launch_tq4_v2_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, pair_lut, mid_o=None,
