@@ -66,13 +66,16 @@ int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block
  * plain-VALU kernel (any GQA group up to 16); MFMA (v_mfma_f32_4x4x4_16b_f16) and XDL
  * (v_mfma_f32_16x16x32_f16) are the matrix-core kernels (GQA group 4 or 8, block_size a
  * power of two >= 16, cache_block_stride a multiple of 16).  AUTO picks XDL when it
- * applies, SIMPLE otherwise.
- * Replaces: the per-version entry points tq4_cuda_v1 .. tq4_cuda_v9 (cuda/tq4_cuda_vN_bind.cpp). */
+ * applies, SIMPLE otherwise.  sinks (fp32 [Hq], may be NULL): per-head sink logits in the
+ * score domain (q.k * attn_scale); split 0 starts its softmax with max = sink, sum = 1
+ * (XDL and SIMPLE kernels; MFMA rejects them).
+ * Replaces: the per-version entry points tq4_cuda_v1 .. tq4_cuda_v9 (cuda/tq4_cuda_vN_bind.cpp);
+ *           the sinks of _tq_decode_stage1 reference/soa_decode_v1.py:134-148. */
 int tq4_stage1_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
                   const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,
                   int Hk, int D, int block_size, int max_blocks_per_seq,
                   int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
-                  int kernel, tq4_stream_t stream);
+                  int kernel, const float *sinks, tq4_stream_t stream);
 
 /*
  * Stage2: merge the non-empty splits of every (b, h):
@@ -96,7 +99,8 @@ int tq4_build_pair_lut(const float *centroids, float *pair_lut, int n_centroids,
 
 /*
  * Full decode step: rotate query into q_rot_ws, build the pair LUT into
- * pair_lut_ws (512 floats), Stage1 into mid_o, Stage2 into out / lse.
+ * pair_lut_ws (512 floats), Stage1 into mid_o, Stage2 into out / lse; sinks as in
+ * tq4_stage1_ex (may be NULL).
  * Replaces: tq4_cuda_v7_full cuda/tq4_cuda_v7.cu:78-84 plus the q rotation of
  *           triton_turboquant_decode_attention reference/soa_decode_v1.py:485-643.
  */
@@ -106,7 +110,7 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
                     float *pair_lut_ws, float *mid_o, void *out, int out_dtype, float *lse,
                     int B, int Hq, int Hk, int D, int block_size, int max_blocks_per_seq,
                     int64_t cache_block_stride, int num_kv_splits, int layout,
-                    float attn_scale, tq4_stream_t stream);
+                    float attn_scale, const float *sinks, tq4_stream_t stream);
 
 /*
  * Cache writer: quantize key / value [N, Hk, D] (dtype TQ4_F32 / TQ4_BF16 / TQ4_F16,

@@ -54,9 +54,11 @@ def decode_kv(cache, blocks, offs, kvh, centroids, is_aos, block_size, num_kv_he
 
 
 def stage1(q_rot, cache, block_table, seq_lens, centroids, num_splits, *, num_kv_heads,
-           block_size=16, is_aos=False, attn_scale=None, mid_o=None):
+           block_size=16, is_aos=False, attn_scale=None, mid_o=None, sinks=None):
     """Return ``mid_o`` float64 ``[B, Hq, S, D+1]``; empty splits keep their prior value
-    (NaN when ``mid_o`` is not given)."""
+    (NaN when ``mid_o`` is not given).  ``sinks`` ``[Hq]``: split 0 of every sequence starts
+    its softmax with max = sink and sum = 1, an extra logit with a zero value
+    (``reference/soa_decode_v1.py:134-148``)."""
     q = np.asarray(q_rot, dtype=np.float64)
     batch, num_q_heads, head_dim = q.shape
     group = num_q_heads // num_kv_heads
@@ -79,8 +81,14 @@ def stage1(q_rot, cache, block_table, seq_lens, centroids, num_splits, *, num_kv
                 heads = slice(kvh * group, (kvh + 1) * group)
                 s = (q[b, heads] @ k.T) * scale
                 m = s.max(axis=1, keepdims=True)
+                sink = None
+                if sinks is not None and sid == 0:
+                    sink = np.asarray(sinks, dtype=np.float64)[heads][:, None]
+                    m = np.maximum(m, sink)
                 p = np.exp(s - m)
                 denom = p.sum(axis=1, keepdims=True)
+                if sink is not None:
+                    denom = denom + np.exp(sink - m)
                 denom = np.where(denom > 0, denom, 1.0)
                 mid_o[b, heads, sid, :head_dim] = (p @ v) / denom
                 mid_o[b, heads, sid, head_dim] = (m + np.log(denom))[:, 0]

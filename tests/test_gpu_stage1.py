@@ -161,3 +161,39 @@ def test_reference_call_shapes(qwen, dev):
     assert_parity(mid_v2.cpu().numpy(), ref)
     assert torch.equal(mid_v2, mid_ext)
     assert_parity(mid_aos.cpu().numpy(), oracle(w, "aos", aos))
+
+
+@pytest.mark.parametrize("kernel", ["xdl", "simple"])
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("group", [4, 8])
+def test_sinks(dev, kernel, layout, group):
+    """Per-head sink logits enter split 0's softmax (max = sink, sum = 1)."""
+    hk = 4
+    w = workloads.small(106, 4, [1, 300, 2049, 77], 8, num_q_heads=hk * group, num_kv_heads=hk)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, hk) if layout == "aos" else w.kv_cache
+    rng = np.random.default_rng(107)
+    sinks = rng.normal(0.0, 3.0, hk * group).astype(np.float32)
+    sinks[1] = -np.inf
+    sinks[2] = 40.0
+    mid = torch.full((w.batch, w.num_q_heads, 8, 129), float("nan"), device=dev)
+    ops.stage1(to_dev(w.q_rot, dev), to_dev(cache, dev), to_dev(w.block_table, dev),
+               to_dev(w.seq_lens, dev), to_dev(w.pair_lut, dev), mid, layout=layout, kernel=kernel,
+               sinks=to_dev(sinks, dev))
+    torch.cuda.synchronize()
+    ref = native_free_oracle(w, cache, layout, sinks)
+    assert_parity(mid.cpu().numpy(), ref)
+
+
+def native_free_oracle(w, cache, layout, sinks):
+    from oracle import stage1 as ostage
+
+    return ostage.stage1(w.q_rot, cache, w.block_table, w.seq_lens, w.centroids, w.num_kv_splits,
+                         num_kv_heads=w.num_kv_heads, is_aos=layout == "aos", sinks=sinks)
+
+
+def test_sinks_rejected_by_the_4x4x4_kernel(dev):
+    w = workloads.small(108, 1, [64], 2)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    with pytest.raises(RuntimeError):
+        ops.stage1(t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens), t(w.pair_lut),
+                   num_kv_splits=2, kernel="mfma", sinks=torch.zeros(32, device=dev))

@@ -144,3 +144,16 @@ def test_backend_decode_entry(dev, layout):
         mod.triton_turboquant_decode_attention(
             t(query), t(cache), t(w.block_table), t(w.seq_lens), t(rot_t.T.copy()), t(w.centroids),
             128 ** -0.5, mse_bits=4, key_packed_size=66, value_quant_bits=4, key_fp8=True)
+    # with sinks (split 0 starts from the head's sink logit)
+    sinks = rng.normal(0.0, 2.0, 32).astype(np.float32)
+    out = mod.triton_turboquant_decode_attention(
+        t(query), t(cache), t(w.block_table), t(w.seq_lens), t(rot_t.T.copy()), t(w.centroids),
+        128 ** -0.5, mse_bits=4, key_packed_size=66, value_quant_bits=4, norm_correction=True,
+        max_num_kv_splits=32, sinks=t(sinks))
+    torch.cuda.synchronize()
+    smid = ostage.stage1(q_rot, cache, w.block_table, w.seq_lens, w.centroids, 32, num_kv_heads=8,
+                         is_aos=layout == "aos", sinks=sinks)
+    so, _ = ostage.stage2(smid, w.seq_lens)
+    err = np.abs(out.float().cpu().numpy() - so).max()
+    print(f"{layout} decode entry with sinks fp16 max-abs {err:.3e}")
+    assert err <= 1e-3

@@ -101,6 +101,44 @@ def test_torch_cpu_restatement_matches_config1_fixture(config1):
         assert np.nanmax(np.abs(got - f[f"mid_{lay}"])) < 2e-6
 
 
+@pytest.mark.parametrize("splits", [1, 4, 32])
+def test_sinks_are_an_extra_logit_with_zero_value(splits):
+    """Sinks: split 0's softmax over the scores plus the sink logit (value 0), checked with
+    torch.softmax / logsumexp over the concatenated logits; Stage2 of the split rows equals
+    unsplit attention with the sink appended once."""
+    w = _small(31, [1, 37, 300, 130], splits)
+    rng = np.random.default_rng(32)
+    sinks = rng.normal(0.0, 3.0, 32)
+    sinks[5] = -np.inf  # a head without a sink
+    sinks[6] = 40.0     # a sink that dominates every score
+    got = stage1.stage1(w.q_rot, w.kv_cache, w.block_table, w.seq_lens, w.centroids, splits,
+                        num_kv_heads=8, sinks=sinks)
+    for b in range(w.batch):
+        a, e = layout.split_range(int(w.seq_lens[b]), splits, 0)
+        tok = np.arange(a, e)
+        blocks, offs = w.block_table[b, tok // 16], tok % 16
+        for kvh in range(8):
+            k, v = stage1.decode_kv(w.kv_cache, blocks, offs, kvh, w.centroids, False, 16, 8, 128)
+            for h in range(kvh * 4, kvh * 4 + 4):
+                logits = torch.from_numpy(np.append(w.q_rot[b, h].astype(np.float64) @ k.T / math.sqrt(128),
+                                                    sinks[h]))
+                p = torch.softmax(logits, 0)[:-1].numpy()
+                assert np.abs(got[b, h, 0, :128] - p @ v).max() < 1e-12
+                assert abs(got[b, h, 0, 128] - torch.logsumexp(logits, 0).item()) < 1e-12
+    o, lse = stage1.stage2(got, w.seq_lens)
+    for b in range(w.batch):
+        tok = np.arange(int(w.seq_lens[b]))
+        blocks, offs = w.block_table[b, tok // 16], tok % 16
+        for kvh in range(8):
+            k, v = stage1.decode_kv(w.kv_cache, blocks, offs, kvh, w.centroids, False, 16, 8, 128)
+            for h in range(kvh * 4, kvh * 4 + 4):
+                logits = torch.from_numpy(np.append(w.q_rot[b, h].astype(np.float64) @ k.T / math.sqrt(128),
+                                                    sinks[h]))
+                p = torch.softmax(logits, 0)[:-1].numpy()
+                assert np.abs(o[b, h] - p @ v).max() < 1e-10
+                assert abs(lse[b, h] - torch.logsumexp(logits, 0).item()) < 1e-10
+
+
 @pytest.mark.parametrize("splits", [1, 3, 4, 16, 32, 64])
 def test_stage2_of_stage1_equals_unsplit_attention(splits):
     w = _small(31, [5, 100, 333], splits)

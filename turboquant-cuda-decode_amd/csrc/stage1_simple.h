@@ -20,9 +20,9 @@ template <int LAYOUT, int G>
 __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
-    const float *__restrict__ pair_lut, float *__restrict__ mid_o, int num_q_heads,
-    int num_kv_heads, int block_size, int max_blocks, int64_t block_stride, int num_splits,
-    float score_scale_log2) {
+    const float *__restrict__ pair_lut, float *__restrict__ mid_o, const float *__restrict__ sinks,
+    int num_q_heads, int num_kv_heads, int block_size, int max_blocks, int64_t block_stride,
+    int num_splits, float score_scale_log2) {
     const int sid = blockIdx.x;
     const int kvh = blockIdx.y;
     const int b = blockIdx.z;
@@ -47,8 +47,10 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
     float m[G], l[G], zl[G], acc[G][2];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        m[h] = -INFINITY;
-        l[h] = 0.f;
+        // split 0 with sinks starts from the head's sink logit: max = sink, sum = 1
+        const bool sink = sinks && sid == 0;
+        m[h] = sink ? sinks[(int64_t)kvh * G + h] * kLog2e : -INFINITY;
+        l[h] = sink ? 1.f : 0.f;
         zl[h] = 0.f;
         acc[h][0] = acc[h][1] = 0.f;
     }

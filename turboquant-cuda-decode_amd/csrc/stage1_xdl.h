@@ -603,9 +603,9 @@ template <int LAYOUT, int G, int WPE>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
-    const float *__restrict__ pair_lut, float *__restrict__ mid_o, int num_q_heads,
-    int num_kv_heads, int block_size_log2, int max_blocks, int64_t block_stride, int num_splits,
-    float score_scale_log2) {
+    const float *__restrict__ pair_lut, float *__restrict__ mid_o, const float *__restrict__ sinks,
+    int num_q_heads, int num_kv_heads, int block_size_log2, int max_blocks, int64_t block_stride,
+    int num_splits, float score_scale_log2) {
     static_assert(G == 4 || G == 8, "GQA group 4 or 8");
     constexpr int TPL = G / 4;
     constexpr int RING = 4;
@@ -659,6 +659,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     half8 bq[8];
 
     State st{__FLT_MAX__, 0.f, 0.f, 1.f};
+    if (sinks && s_lo == 0) {
+        // split 0 starts from the head's sink logit: max = sink, sum = 1 (one lane per head,
+        // lane h, holds it; the sums are totalled over the lanes n = h (mod G))
+        st.negm = -sinks[(int64_t)kvh * G + (lc.n & (G - 1))] * kLog2e;
+        st.l = lane < G ? 1.f : 0.f;
+    }
     floatx4 acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)

@@ -81,6 +81,7 @@ struct Stage1Args {
     int64_t stride;
     int S, layout;
     float scale;
+    const float *sinks = nullptr;  // [Hq] sink logits of split 0, or null
 };
 
 int check_stage1(const Stage1Args &a) {
@@ -109,7 +110,7 @@ int check_stage1(const Stage1Args &a) {
 template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t st) {
     const dim3 grid(a.S, a.Hk, a.B);
     launch(&tq4::stage1_simple_kernel<LAYOUT, G>, grid, dim3(tq4::kWave), st,
-                       a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk, a.bs,
+                       a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.sinks, a.Hq, a.Hk, a.bs,
                        a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
 
@@ -180,7 +181,7 @@ template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st
     const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>()>;
     const dim3 grid(a.Hk, xdl_waves<LAYOUT, G>(a), a.B);
     launch(kernel, grid, dim3(tq4::kWave), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
-                       a.mid_o, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks, a.stride, a.S,
+                       a.mid_o, a.sinks, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks, a.stride, a.S,
                        a.scale * tq4::kLog2e);
 }
 
@@ -244,6 +245,8 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     // AUTO: the 16x16x32 kernel wherever the MFMA kernels apply (both layouts), else VALU.
     if (kernel == TQ4_KERNEL_AUTO)
         kernel = mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE;
+    if (kernel == TQ4_KERNEL_MFMA && a.sinks)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_ex: sinks need the XDL or the VALU kernel");
     if (kernel == TQ4_KERNEL_MFMA)
         return a.layout == TQ4_LAYOUT_SOA ? dispatch_mfma<0>(a, st) : dispatch_mfma<1>(a, st);
     if (kernel == TQ4_KERNEL_SIMPLE)
@@ -293,7 +296,7 @@ int tq4_time_next_launch(void *start_event, void *stop_event) {
     return ok();
 }
 
-int tq4_abi_version(void) { return 100; }
+int tq4_abi_version(void) { return 101; }
 
 const char *tq4_last_error(void) { return g_err; }
 
@@ -301,10 +304,10 @@ int tq4_stage1_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *bl
                   const int32_t *seq_lens, const float *pair_lut, float *mid_o, int B, int Hq,
                   int Hk, int D, int block_size, int max_blocks_per_seq,
                   int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
-                  int kernel, tq4_stream_t stream) {
+                  int kernel, const float *sinks, tq4_stream_t stream) {
     const Stage1Args a{q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o, B, Hq, Hk, D,
                        block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits,
-                       layout, attn_scale};
+                       layout, attn_scale, sinks};
     return run_stage1(a, kernel, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -315,7 +318,7 @@ int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block
                tq4_stream_t stream) {
     return tq4_stage1_ex(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o, B, Hq, Hk, D,
                          block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits,
-                         layout, attn_scale, TQ4_KERNEL_AUTO, stream);
+                         layout, attn_scale, TQ4_KERNEL_AUTO, nullptr, stream);
 }
 
 int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_dtype,
@@ -371,7 +374,7 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
                     float *pair_lut_ws, float *mid_o, void *out, int out_dtype, float *lse,
                     int B, int Hq, int Hk, int D, int block_size, int max_blocks_per_seq,
                     int64_t cache_block_stride, int num_kv_splits, int layout,
-                    float attn_scale, tq4_stream_t stream) {
+                    float attn_scale, const float *sinks, tq4_stream_t stream) {
     if (!centroids || !pair_lut_ws)
         return fail(TQ4_E_INVALID, "tq4_full_decode: null pointer argument");
     // one launch rotates the query and writes the pair LUT
@@ -382,9 +385,10 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
     // When the Stage1 kernel gives each (sequence, kv-head) one wave anyway, that wave runs
     // the whole sequence as one split: the same attention (up to rounding), without writing
     // and re-reading num_kv_splits rows per head; Stage2 then only converts the row.
+    // (with sinks too: the sink enters split 0, the only split then)
     Stage1Args a{q_rot_ws, kv_cache, block_table, seq_lens, pair_lut_ws, mid_o, B, Hq, Hk, D,
                  block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
-                 attn_scale};
+                 attn_scale, sinks};
     if (num_kv_splits > 1 && check_stage1(a) == TQ4_OK && auto_xdl_waves(a) == 1)
         a.S = 1;
     rc = run_stage1(a, TQ4_KERNEL_AUTO, reinterpret_cast<hipStream_t>(stream));

@@ -34,12 +34,12 @@ _handle = None
 _p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 _SIGS = {
     "tq4_stage1": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p],
-    "tq4_stage1_ex": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _i, _p],
+    "tq4_stage1_ex": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _i, _p, _p],
     "tq4_stage2": [_p, _p, _p, _i, _p, _i, _i, _i, _i, _p],
     "tq4_rotate_query": [_p, _i, _p, _p, _i, _i, _p],
     "tq4_build_pair_lut": [_p, _p, _i, _p],
     "tq4_full_decode": [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i,
-                        _i, _i64, _i, _i, _f, _p],
+                        _i, _i64, _i, _i, _f, _p, _p],
     "tq4_store": [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _p],
     "tq4_last_error": [],
     "tq4_abi_version": [],

@@ -67,12 +67,21 @@ def pair_lut_device(centroids: torch.Tensor) -> torch.Tensor:
     return lut
 
 
+def _check_sinks(sinks, num_q_heads, device):
+    if sinks is None:
+        return None
+    _check_tensor(sinks, "sinks", torch.float32)
+    _require(sinks.numel() == num_q_heads and sinks.device == device, "sinks must be fp32 [Hq]")
+    return sinks.data_ptr()
+
+
 def stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o=None, *, num_kv_splits=None,
-           layout="soa", attn_scale=None, kernel="auto"):
+           layout="soa", attn_scale=None, kernel="auto", sinks=None):
     """Stage1 over the 4-bit paged cache; returns ``mid_o [B, Hq, S, D+1]`` (fp32).
 
     ``S`` comes from ``mid_o`` when given, else from ``num_kv_splits``.  Empty splits
-    leave their ``mid_o`` rows untouched.
+    leave their ``mid_o`` rows untouched.  ``sinks`` (fp32 ``[Hq]``): per-head sink logits
+    that split 0's softmax starts from (``reference/soa_decode_v1.py:134-148``).
     """
     for t, n, dt in ((q_rot, "q_rot", torch.float32), (kv_cache, "kv_cache", torch.uint8),
                      (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
@@ -101,10 +110,12 @@ def stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o=None, *, num_
     _require(len(devs) == 1, "all tensors must be on the same device")
     scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
     _require(kernel in KERNELS, f"kernel must be one of {sorted(KERNELS)}")
+    sinks_ptr = _check_sinks(sinks, Hq, q_rot.device)
     rc = _lib.load().tq4_stage1_ex(
         q_rot.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
         pair_lut.data_ptr(), mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1),
-        kv_cache.stride(0), S, _layout_id(layout), scale, KERNELS[kernel], _stream(q_rot.device))
+        kv_cache.stride(0), S, _layout_id(layout), scale, KERNELS[kernel], sinks_ptr,
+        _stream(q_rot.device))
     _lib.check(rc, "tq4_stage1")
     return mid_o
 
@@ -201,7 +212,7 @@ class DecodeWorkspace:
 
 
 def full_decode(query, rotation_t, kv_cache, block_table, seq_lens, centroids, num_kv_splits, *,
-                layout="soa", out_dtype=None, attn_scale=None, workspace=None):
+                layout="soa", out_dtype=None, attn_scale=None, workspace=None, sinks=None):
     """Rotation + pair LUT + Stage1 + Stage2 in four launches; returns ``(out, lse)``.
 
     ``out`` is in ``out_dtype`` (default: the query dtype, as ``reference/soa_decode_v1.py:643``).
@@ -222,12 +233,13 @@ def full_decode(query, rotation_t, kv_cache, block_table, seq_lens, centroids, n
     _require(ws.out.dtype == out_dtype and ws.mid_o.shape[:3] == (B, Hq, num_kv_splits),
              "workspace does not match this call")
     scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
+    sinks_ptr = _check_sinks(sinks, Hq, query.device)
     rc = _lib.load().tq4_full_decode(
         query.data_ptr(), DTYPES[query.dtype], rotation_t.data_ptr(), centroids.data_ptr(),
         kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), ws.q_rot.data_ptr(),
         ws.pair_lut.data_ptr(), ws.mid_o.data_ptr(), ws.out.data_ptr(), DTYPES[out_dtype],
         ws.lse.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), kv_cache.stride(0),
-        num_kv_splits, _layout_id(layout), scale, _stream(query.device))
+        num_kv_splits, _layout_id(layout), scale, sinks_ptr, _stream(query.device))
     _lib.check(rc, "tq4_full_decode")
     return ws.out, ws.lse
 
@@ -253,14 +265,12 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
 
     Caller buffers are used when they fit (``mid_o_buf`` fp32 ``[>=B, Hq, S, D+1]``,
     ``output_buf`` ``[>=B, Hq, D]`` in the query dtype, ``lse_buf`` fp32 ``[>=B, Hq]``); the
-    rotated query and the pair LUT live on ``buf_holder`` when one is given.  Built for the
-    4-bit ``turboquant_4bit_nc`` cache: FP8 keys, other bit widths, sinks and AoS without
-    norm correction raise ``NotImplementedError``.
+    rotated query and the pair LUT live on ``buf_holder`` when one is given; ``sinks``
+    (fp32 ``[Hq]``) enter split 0.  Built for the 4-bit ``turboquant_4bit_nc`` cache: FP8
+    keys, other bit widths and AoS without norm correction raise ``NotImplementedError``.
     """
     if key_fp8:
         raise NotImplementedError("FP8 keys (the k8v4 presets) are not built")
-    if sinks is not None:
-        raise NotImplementedError("attention sinks are not built")
     _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
     _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
     if layout == "aos" and not norm_correction:
@@ -294,7 +304,8 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
     if ws.lse is None:
         ws.lse = held("_tq_lse_buf", (B, Hq), torch.float32)
     out, _ = full_decode(query.contiguous(), PiT, kv_cache, block_table, seq_lens, centroids, S,
-                         layout=layout, out_dtype=query.dtype, attn_scale=scale, workspace=ws)
+                         layout=layout, out_dtype=query.dtype, attn_scale=scale, workspace=ws,
+                         sinks=sinks)
     return out
 
 
