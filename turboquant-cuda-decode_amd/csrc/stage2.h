@@ -62,8 +62,8 @@ constexpr int kRotMfmaRows = 16 * kRotWaves;  // rows per workgroup
 constexpr int kRotPt = kHeadDim + 8;           // LDS row of rot_t^T (halves), 16-byte aligned
 typedef _Float16 rot_half8 __attribute__((ext_vector_type(8)));
 
-template <typename InT>
-__device__ __forceinline__ void rot_a_operands(const InT *p, rot_half8 &hi, rot_half8 &lo) {
+template <typename InT, typename V8>
+__device__ __forceinline__ void rot_a_operands(const V8 &p, rot_half8 &hi, rot_half8 &lo) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const float x = to_float<InT>(p[j]);
@@ -78,37 +78,65 @@ __global__ __launch_bounds__(kWave *kRotWaves) void rotate_mfma_kernel(const InT
                                                                         float *__restrict__ q_rot, int rows,
                                                                         const float *__restrict__ centroids,
                                                                         float *__restrict__ pair_lut) {
-    // optional side task of the first workgroup: the pair LUT (row lo * 16 + hi = (c[lo], c[hi]))
-    if (pair_lut && blockIdx.x == 0 && threadIdx.x < 256) {
-        pair_lut[2 * threadIdx.x] = centroids[threadIdx.x / 16];
-        pair_lut[2 * threadIdx.x + 1] = centroids[threadIdx.x % 16];
-    }
     __shared__ __align__(16) _Float16 pt_hi[kHeadDim * kRotPt];  // [col][k]
     __shared__ __align__(16) _Float16 pt_lo[kHeadDim * kRotPt];
-    // thread (c, kg): rot_t[8kg .. 8kg+7][c] (coalesced over c) -> one 16-byte LDS write each
-    for (int i = threadIdx.x; i < kHeadDim * (kHeadDim / 8); i += blockDim.x) {
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int n = lane & 15, g = lane >> 4;
+    const int r0 = blockIdx.x * kRotMfmaRows + 16 * wave;
+    // side task of the first workgroup: the pair LUT (row lo * 16 + hi = (c[lo], c[hi])),
+    // loaded here and stored at the end, off the staging's critical path
+    static_assert(kWave * kRotWaves == 256, "one thread per pair-LUT row");
+    const bool lut_task = pair_lut && blockIdx.x == 0;
+    float c_lo = 0.f, c_hi = 0.f;
+    if (lut_task) {
+        c_lo = centroids[threadIdx.x / 16];
+        c_hi = centroids[threadIdx.x % 16];
+    }
+    // the query rows go out first (rows past the end repeat the last one, not stored)
+    const int ra = min(r0 + n, rows - 1);
+    // 8 consecutive elements per (kb, lane): 16-byte loads (the query is 16-byte aligned)
+    typedef InT in8 __attribute__((ext_vector_type(8)));
+    in8 qv[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+        qv[kb] = *reinterpret_cast<const in8 *>(query + (int64_t)ra * kHeadDim + 32 * kb + 8 * g);
+    // thread (c, kg): rot_t[8kg .. 8kg+7][c] (coalesced over c) -> one 16-byte LDS write
+    // into each part.  All 64 loads of a thread go out before the first conversion.
+    constexpr int kIters = kHeadDim * (kHeadDim / 8) / (kWave * kRotWaves);
+    float wv[kIters][8];
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+        const int i = threadIdx.x + it * kWave * kRotWaves;
+        const int c = i % kHeadDim, kg = i / kHeadDim;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            wv[it][j] = rot_t[(8 * kg + j) * kHeadDim + c];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+        const int i = threadIdx.x + it * kWave * kRotWaves;
         const int c = i % kHeadDim, kg = i / kHeadDim;
         rot_half8 h, l;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float w = rot_t[(8 * kg + j) * kHeadDim + c];
-            h[j] = (_Float16)w;
-            l[j] = (_Float16)(w - (float)h[j]);
+            h[j] = (_Float16)wv[it][j];
+            l[j] = (_Float16)(wv[it][j] - (float)h[j]);
         }
         *reinterpret_cast<rot_half8 *>(pt_hi + c * kRotPt + 8 * kg) = h;
         *reinterpret_cast<rot_half8 *>(pt_lo + c * kRotPt + 8 * kg) = l;
     }
     __syncthreads();
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int n = lane & 15, g = lane >> 4;
-    const int r0 = blockIdx.x * kRotMfmaRows + 16 * wave;
+    if (lut_task) {
+        pair_lut[2 * threadIdx.x] = c_lo;
+        pair_lut[2 * threadIdx.x + 1] = c_hi;
+    }
     if (r0 >= rows)
         return;
-    const int ra = min(r0 + n, rows - 1);  // rows past the end repeat the last one (not stored)
     rot_half8 a_hi[4], a_lo[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-        rot_a_operands<InT>(query + (int64_t)ra * kHeadDim + 32 * kb + 8 * g, a_hi[kb], a_lo[kb]);
+        rot_a_operands<InT>(qv[kb], a_hi[kb], a_lo[kb]);
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
