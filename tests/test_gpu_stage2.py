@@ -157,3 +157,42 @@ def test_backend_decode_entry(dev, layout):
     err = np.abs(out.float().cpu().numpy() - so).max()
     print(f"{layout} decode entry with sinks fp16 max-abs {err:.3e}")
     assert err <= 1e-3
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_full_decode_fused_one_split_path(dev, out_dtype):
+    """B256 x 8 kv-heads: one wave per (sequence, kv-head), so the full step runs one split
+    per sequence and the Stage1 kernel writes the output rows itself.  Bit-identical to
+    Stage1 with one split + Stage2 (including empty sequences: NaN rows, -inf LSE) and
+    within the oracle's fp32 gate plus the output type's rounding."""
+    rng = np.random.default_rng(207)
+    lens = rng.integers(0, 1500, 256).astype(np.int32)
+    lens[[3, 100, 255]] = 0
+    lens[[4, 7]] = 1
+    w = workloads.small(207, 256, lens, 16)
+    query = rng.standard_normal((256, 32, 128)).astype(np.float32)
+    rot_t = workloads.random_orthogonal(rng, 128)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    q, r = t(query).half(), t(rot_t)
+    cache, bt, sl, cents = t(w.kv_cache), t(w.block_table), t(w.seq_lens), t(w.centroids)
+    out, lse = ops.full_decode(q, r, cache, bt, sl, cents, 16, out_dtype=out_dtype)
+    q_rot = torch.empty(256, 32, 128, device=dev)
+    ops.rotate_query(q, r, q_rot)
+    mid = ops.stage1(q_rot, cache, bt, sl, ops.pair_lut_device(cents), num_kv_splits=1)
+    ref_out, ref_lse = ops.stage2(mid, sl, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    a, b = out.float().cpu().numpy(), ref_out.float().cpu().numpy()
+    assert np.array_equal(np.isnan(a), np.isnan(b)) and np.isnan(a[[3, 100, 255]]).all()
+    assert np.array_equal(a[~np.isnan(a)], b[~np.isnan(b)]), "fused rows differ from Stage1 + Stage2"
+    assert np.array_equal(lse.cpu().numpy(), ref_lse.cpu().numpy())
+    assert np.isneginf(lse.cpu().numpy()[[3, 100, 255]]).all()
+    qr = (query.astype(np.float16).astype(np.float64) @ rot_t.astype(np.float64)).astype(np.float32)
+    omid = native.stage1(qr, w.kv_cache, w.block_table, w.seq_lens, w.centroids, 16, num_kv_heads=8)
+    ro, _ = native.stage2(omid, w.seq_lens)
+    live = lens > 0
+    # fp32 gate 1e-4, plus the output type's rounding: unit roundoff 2^-p of its p-bit
+    # significand (bf16 p = 8, fp16 p = 11)
+    half_ulp = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 0.0}[out_dtype]
+    excess = np.abs(a[live] - ro[live]) - (1e-4 + half_ulp * np.abs(ro[live]))
+    print(f"fused full decode {out_dtype} max-abs {np.abs(a[live] - ro[live]).max():.3e}")
+    assert excess.max() <= 0

@@ -564,6 +564,51 @@ __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc
         img[lc.n * Cap::head_floats + j * (kHeadDim + 1) + kHeadDim] = -st.negm * kLn2 + logf(safe_l);
 }
 
+// Output element conversion of the fused epilogue (the same roundings as Stage2's).
+__device__ __forceinline__ void put_out(void *out, int dtype, int64_t i, float v) {
+    if (dtype == kOutBf16)
+        static_cast<__bf16 *>(out)[i] = (__bf16)v;
+    else if (dtype == kOutF16)
+        static_cast<_Float16 *>(out)[i] = (_Float16)v;
+    else
+        static_cast<float *>(out)[i] = v;
+}
+
+// One split per sequence: with a single live split Stage2's merge is the identity (weight
+// exp(0) = 1, sum 1), so the wave writes the final output rows and LSE itself -- the same
+// values Stage2 would write, without the mid_o round trip.
+template <int G>
+__device__ __forceinline__ void emit_output(const State &st, const floatx4 (&acc)[8], const LaneConst &lc,
+                                            void *out, int out_dtype, float *lse, int64_t row0) {
+    const float lt = head_sum<G>(st.l);
+    const float zt = head_sum<G>(st.z);
+    const float safe_l = lt > 0.f ? lt : 1.f;
+    const int hA = 2 * (lc.g >> 1) + (G == 8 ? 4 * (lc.g & 1) : 0);
+    const float inv_a = __builtin_amdgcn_rcpf(__shfl(safe_l, hA, kWave));
+    const float inv_b = __builtin_amdgcn_rcpf(__shfl(safe_l, hA + 1, kWave));
+    const float z_a = __shfl(zt, hA, kWave), z_b = __shfl(zt, hA + 1, kWave);
+    float oa[8], ob[8];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
+        const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
+        oa[2 * m] = fmaf(xa, 16777216.0f, z_a) * inv_a;
+        ob[2 * m] = fmaf(xb, 16777216.0f, z_b) * inv_b;
+        oa[2 * m + 1] = fmaf(ya - xa, 1048576.0f, z_a) * inv_a;
+        ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
+    }
+    if (G == 8 || (lc.g & 1) == 0) {
+        const int64_t ra = (row0 + hA) * kHeadDim + 8 * lc.n, rb = ra + kHeadDim;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            put_out(out, out_dtype, ra + i, oa[i]);
+            put_out(out, out_dtype, rb + i, ob[i]);
+        }
+    }
+    if (lc.g == 0 && lc.n < G)
+        lse[row0 + lc.n] = -st.negm * kLn2 + logf(safe_l);
+}
+
 // Write image slots 0 .. ns-1 to the rows of splits s0 .. s0+ns-1.  Rows of one head and
 // consecutive splits are consecutive in mid_o [B, Hq, S, D + 1], so head h's slots are one
 // run of ns * 129 floats.  One wave: its LDS accesses complete in program order, so only
@@ -599,11 +644,15 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
 // split ends fall on 4-stage boundaries (after an odd stage's PV).  After a split's last
 // stage the wave puts its rows into the LDS image (flushed to mid_o when full and after
 // the wave's last split) and restarts the softmax state and the accumulators.
-template <int LAYOUT, int G, int WPE>
+//
+// FUSED (launched with one split per sequence and one wave per (sequence, kv-head)): the
+// wave writes the final output rows (out, out_dtype) and LSE instead of mid_o rows.
+template <int LAYOUT, int G, int WPE, bool FUSED>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
     const float *__restrict__ pair_lut, float *__restrict__ mid_o, const float *__restrict__ sinks,
+    void *__restrict__ out, int out_dtype, float *__restrict__ lse,
     int num_q_heads, int num_kv_heads, int block_size_log2, int max_blocks, int64_t block_stride,
     int num_splits, float score_scale_log2) {
     static_assert(G == 4 || G == 8, "GQA group 4 or 8");
@@ -642,6 +691,17 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const int s_lo = (int)((int64_t)wid * num_splits / nw);
     const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
     const int s_hi = min((int)((int64_t)(wid + 1) * num_splits / nw), live);
+    if constexpr (FUSED) {
+        if (live == 0) {
+            // an empty sequence: what Stage2 writes for it (0 / 0 and ln 0)
+            const int64_t r0 = ((int64_t)b * num_q_heads + kvh * G) * kHeadDim;
+            for (int i = lane; i < G * kHeadDim; i += kWave)
+                put_out(out, out_dtype, r0 + i, __builtin_nanf(""));
+            if (lane < G)
+                lse[(int64_t)b * num_q_heads + kvh * G + lane] = -__builtin_inff();
+            return;
+        }
+    }
     if (s_lo >= s_hi)
         return;
 
@@ -839,7 +899,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                 }
                 j += RING;
             } while (j < stop);
-            if (j == pos_base + cur_stop) {
+            // (FUSED: the only split ends with the stream; its rows are written after the loop)
+            if (!FUSED && j == pos_base + cur_stop) {
                 stash_split<G, Cap>(st, acc, lc, img, cur - img_s0);
                 if (cur + 1 == s_hi || cur + 1 - img_s0 == Cap::splits) {
                     flush_splits<G, Cap>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
@@ -860,6 +921,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                 break;
         }
     }
+    if constexpr (FUSED)
+        emit_output<G>(st, acc, lc, out, out_dtype, lse, row0);
 }
 
 }  // namespace xdl

@@ -82,7 +82,13 @@ struct Stage1Args {
     int S, layout;
     float scale;
     const float *sinks = nullptr;  // [Hq] sink logits of split 0, or null
+    // set: one split per sequence, the XDL kernel writes the final rows (Stage2 fused)
+    void *out = nullptr;
+    int out_dtype = TQ4_F32;
+    float *lse = nullptr;
 };
+static_assert(tq4::kOutF32 == TQ4_F32 && tq4::kOutBf16 == TQ4_BF16 && tq4::kOutF16 == TQ4_F16,
+              "output type ids");
 
 int check_stage1(const Stage1Args &a) {
     if (!a.q_rot || !a.cache || !a.bt || !a.seq_lens || !a.lut || !a.mid_o)
@@ -173,16 +179,18 @@ template <int LAYOUT, int G> constexpr int xdl_waves_per_simd() {
 
 template <int LAYOUT, int G> int xdl_waves(const Stage1Args &a) {
     static int slots = 0;
-    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>()>;
+    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>(), false>;
     return waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots);
 }
 
 template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
-    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>()>;
+    constexpr int wpe = xdl_waves_per_simd<LAYOUT, G>();
     const dim3 grid(a.Hk, xdl_waves<LAYOUT, G>(a), a.B);
+    const auto kernel = a.out ? &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, true>
+                              : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false>;
     launch(kernel, grid, dim3(tq4::kWave), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
-                       a.mid_o, a.sinks, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks, a.stride, a.S,
-                       a.scale * tq4::kLog2e);
+           a.mid_o, a.sinks, a.out, a.out_dtype, a.lse, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks,
+           a.stride, a.S, a.scale * tq4::kLog2e);
 }
 
 template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
@@ -384,13 +392,24 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
         return rc;
     // When the Stage1 kernel gives each (sequence, kv-head) one wave anyway, that wave runs
     // the whole sequence as one split: the same attention (up to rounding), without writing
-    // and re-reading num_kv_splits rows per head; Stage2 then only converts the row.
-    // (with sinks too: the sink enters split 0, the only split then)
+    // and re-reading num_kv_splits rows per head (with sinks too: the sink enters split 0,
+    // the only split then).
     Stage1Args a{q_rot_ws, kv_cache, block_table, seq_lens, pair_lut_ws, mid_o, B, Hq, Hk, D,
                  block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
                  attn_scale, sinks};
-    if (num_kv_splits > 1 && check_stage1(a) == TQ4_OK && auto_xdl_waves(a) == 1)
+    // With one split per sequence Stage2's merge is the identity, so the Stage1 kernel
+    // writes the output rows and LSE itself (mid_o is not written then).
+    if (check_stage1(a) == TQ4_OK && auto_xdl_waves(a) == 1) {
+        if (!out || !lse)
+            return fail(TQ4_E_INVALID, "tq4_full_decode: null pointer argument");
+        if (out_dtype != TQ4_F32 && out_dtype != TQ4_BF16 && out_dtype != TQ4_F16)
+            return fail(TQ4_E_INVALID, "tq4_full_decode: out_dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
         a.S = 1;
+        a.out = out;
+        a.out_dtype = out_dtype;
+        a.lse = lse;
+        return run_stage1(a, TQ4_KERNEL_XDL, reinterpret_cast<hipStream_t>(stream));
+    }
     rc = run_stage1(a, TQ4_KERNEL_AUTO, reinterpret_cast<hipStream_t>(stream));
     if (rc)
         return rc;

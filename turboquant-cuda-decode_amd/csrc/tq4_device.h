@@ -12,6 +12,8 @@ constexpr int kSoaRecord = kHeadDim;        // SoA data record: K codes | V code
 constexpr int kAosSlot = kHeadDim + 6;      // AoS slot: K | norm | V | scale | zero
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
+// Output element types of the fused epilogue (the ABI's TQ4_F32 / TQ4_BF16 / TQ4_F16).
+constexpr int kOutF32 = 0, kOutBf16 = 1, kOutF16 = 2;
 constexpr float kLn2 = 0.6931471805599453f;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
