@@ -107,7 +107,7 @@ __device__ __forceinline__ float half_at(uint32_t w, int hi) {
 // ds_read_b64 straight into half of a QK^T operand; AoS adds a second table of
 // c[lo]^2 + c[hi]^2 (fp32) for the norm correction.
 template <int LAYOUT> struct KTable {
-    static constexpr int words = LAYOUT == 0 ? 512 : 768;
+    static constexpr int words = 512;
 };
 
 // Pair-LUT rows of the lane's table entries e = lane + 64 i (loaded before the build so
@@ -134,8 +134,6 @@ __device__ __forceinline__ void build_key_table(uint32_t *tbl, const LutRows &v,
         const uint32_t p_lo = split_f16(c_lo), p_hi = split_f16(c_hi);
         tbl[2 * e] = (p_lo & 0xFFFFu) | (p_hi << 16);
         tbl[2 * e + 1] = (p_lo >> 16) | (p_hi & 0xFFFF0000u);
-        if constexpr (LAYOUT == 1)
-            tbl[512 + e] = fbits(c_lo * c_lo + c_hi * c_hi);
     }
 }
 
@@ -323,9 +321,17 @@ __device__ __forceinline__ KOps lookup_tile(const uint4 &k, const uint32_t *ktab
         r.e[b] = t2[(kw[b >> 2] >> (8 * (b & 3))) & 0xFFu];
     r.csq = 0.f;
     if constexpr (LAYOUT == 1) {
+        // c_lo^2 + c_hi^2 of every byte from its own entry: c = h + l (f16 parts), so
+        // sum c^2 = sum h.h + 2 sum h.l (+ l.l, below fp32 rounding); f16 products are exact
+        float hh = 0.f, hl = 0.f;
 #pragma unroll
-        for (int b = 0; b < 16; ++b)
-            r.csq += bitsf(ktab[512 + ((kw[b >> 2] >> (8 * (b & 3))) & 0xFFu)]);
+        for (int b = 0; b < 16; ++b) {
+            const auto h = __builtin_bit_cast(__fp16 __attribute__((ext_vector_type(2))), r.e[b].x);
+            const auto l = __builtin_bit_cast(__fp16 __attribute__((ext_vector_type(2))), r.e[b].y);
+            hh = __builtin_amdgcn_fdot2(h, h, hh, false);
+            hl = __builtin_amdgcn_fdot2(h, l, hl, false);
+        }
+        r.csq = fmaf(2.f, hl, hh);
     }
     return r;
 }
