@@ -736,13 +736,19 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     for (int j = 0; j < 8; ++j)
         acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // stream positions of a split with n tiles: n rounded up to a whole ring turn
-    auto ring_padded = [](int n) { return (n + RING - 1) & ~(RING - 1); };
-    int total = 0;
-    for (int s = s_lo; s < s_hi; ++s) {
+    // Stream positions of split s: its tiles rounded up to an even count (a split ends
+    // after an odd stage, with the PV of its last pair); the wave's last split takes the
+    // extra positions that make the stream a whole number of ring turns.
+    auto split_tiles = [&](int s) {
         const int st0 = s * split_len, en = min(st0 + split_len, seq_len);
-        total += ring_padded(((en - 1) >> 4) - (st0 >> 4) + 1);
-    }
+        return ((en - 1) >> 4) - (st0 >> 4) + 1;
+    };
+    int total = 0;
+    for (int s = s_lo; s < s_hi; ++s)
+        total += (split_tiles(s) + 1) & ~1;
+    const int tail = ((total + RING - 1) & ~(RING - 1)) - total;
+    total += tail;
+    auto split_stop = [&](int s) { return ((split_tiles(s) + 1) & ~1) + (s == s_hi - 1 ? tail : 0); };
 
     const LaneOffsets off = lane_offsets<LAYOUT, G>(lc.n, lc.g, kvh, num_kv_heads, block_size);
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
@@ -754,7 +760,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     int img_s0 = s_lo;  // split of image slot 0
     int cur_start = cur * split_len;
     int cur_end = min(cur_start + split_len, seq_len);
-    int cur_stop = ring_padded(((cur_end - 1) >> 4) - (cur_start >> 4) + 1);
+    int cur_stop = split_stop(cur);
 
     // Lane i of base_lo / base_hi holds the address of the 16-token piece at stream
     // position j0 + i of the current chunk (its KV block plus the piece's offset), lane i
@@ -849,7 +855,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                     tile_lane = tf + min(o, nt - 1);
                     mask_lane = o < nt ? tile_lane : -(1 << 24);  // padding: no valid token
                 }
-                base += ring_padded(nt);
+                base += split_stop(s);
             }
         }
         {
@@ -891,41 +897,37 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         }
         issue_kpos(kr[0], base_lo, base_hi, min(j0 + RING, last));
         int j = j0;
-        while (true) {
-            const int stop = min(pos_base + cur_stop, last + 1);
-            do {
+        do {
 #pragma unroll
-                for (int k = 0; k < RING; ++k) {
-                    stage(k, vr[(k + RING - 1) % RING], vr[k], kr[(k + 2) % RING], mask_lane, j + k);
-                    issue_kpos(kr[(k + 1) % RING], base_lo, base_hi, min(j + k + 1 + RING, last));
-                    if (k & 1) {
-                        issue_vpos(vr[k - 1], base_lo, base_hi, moff_lane, min(j + k - 1 + RING, last));
-                        issue_vpos(vr[k], base_lo, base_hi, moff_lane, min(j + k + RING, last));
+            for (int k = 0; k < RING; ++k) {
+                stage(k, vr[(k + RING - 1) % RING], vr[k], kr[(k + 2) % RING], mask_lane, j + k);
+                issue_kpos(kr[(k + 1) % RING], base_lo, base_hi, min(j + k + 1 + RING, last));
+                if (k & 1) {
+                    issue_vpos(vr[k - 1], base_lo, base_hi, moff_lane, min(j + k - 1 + RING, last));
+                    issue_vpos(vr[k], base_lo, base_hi, moff_lane, min(j + k + RING, last));
+                    // a split ends after an odd stage (FUSED: the only split ends with the
+                    // stream; its rows are written after the loop)
+                    if (!FUSED && j + k + 1 == pos_base + cur_stop) {
+                        stash_split<G, Cap>(st, acc, lc, img, cur - img_s0);
+                        if (cur + 1 == s_hi || cur + 1 - img_s0 == Cap::splits) {
+                            flush_splits<G, Cap>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
+                            img_s0 = cur + 1;
+                        }
+                        // fresh softmax state; the next split's first max change owes nothing
+                        st = State{__FLT_MAX__, 0.f, 0.f, 1.f};
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+                        pos_base = j + k + 1;
+                        ++cur;
+                        cur_start = cur * split_len;
+                        cur_end = min(cur_start + split_len, seq_len);
+                        cur_stop = split_stop(cur);
                     }
                 }
-                j += RING;
-            } while (j < stop);
-            // (FUSED: the only split ends with the stream; its rows are written after the loop)
-            if (!FUSED && j == pos_base + cur_stop) {
-                stash_split<G, Cap>(st, acc, lc, img, cur - img_s0);
-                if (cur + 1 == s_hi || cur + 1 - img_s0 == Cap::splits) {
-                    flush_splits<G, Cap>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
-                    img_s0 = cur + 1;
-                }
-                // fresh softmax state; the next split's first max change owes nothing
-                st = State{__FLT_MAX__, 0.f, 0.f, 1.f};
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-                pos_base = j;
-                ++cur;
-                cur_start = cur * split_len;
-                cur_end = min(cur_start + split_len, seq_len);
-                cur_stop = ring_padded(((cur_end - 1) >> 4) - (cur_start >> 4) + 1);
             }
-            if (j > last)
-                break;
-        }
+            j += RING;
+        } while (j <= last);
     }
     if constexpr (FUSED)
         emit_output<G>(st, acc, lc, out, out_dtype, lse, row0);
