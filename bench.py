@@ -122,7 +122,7 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
-def store_times(dev, flush, timer, reps=30):
+def store_times(dev, flush, timer, reps=30, only=None):
     """Cache writer (tq4_store, SoA, bf16 K/V, norm correction) cold, kernel duration: one
     decode step (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  Bytes per (token,
     kv-head): 2 x 256 read + 134 written, plus 4 of slot mapping per token."""
@@ -138,6 +138,8 @@ def store_times(dev, flush, timer, reps=30):
     rot, c, m = t(workloads.random_orthogonal(rng, 128)), t(cents), t(mids)
     out = {}
     for name, n_tok in (("decode_b64", 64), ("prefill_n8192", 8192)):
+        if only is not None and name != only:
+            continue
         key = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
         val = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
         n_blocks = (n_tok + 15) // 16 + 4
@@ -162,8 +164,9 @@ def store_times(dev, flush, timer, reps=30):
 
 def full_decode_time(dev, flush, timer, reps=30):
     """Whole decode step (fp16 query -> rotation + pair LUT -> Stage1 -> Stage2 -> fp16
-    out) at B=256 x ctx 2048, 32/8 heads, 16 splits, cold.  Bytes: KV of every token
-    and kv-head + query in + output and LSE out + block table."""
+    out) at B=256 x ctx 2048, 32/8 heads, 16 splits, cold, timed by events around the
+    step (it is two or more launches).  Bytes: KV of every token and kv-head + fp16 query
+    in + fp16 output and LSE out + block table + rotation."""
     import numpy as np
     import torch
 
@@ -171,7 +174,7 @@ def full_decode_time(dev, flush, timer, reps=30):
 
     w = workloads.full_b256_ctx2048()
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-    args = (t(w.query), t(w.rotation_t), t(w.kv_cache), t(w.block_table), t(w.seq_lens),
+    args = (t(w.query).half(), t(w.rotation_t), t(w.kv_cache), t(w.block_table), t(w.seq_lens),
             t(w.centroids), w.num_kv_splits)
     ws = ops.DecodeWorkspace(w.batch, w.num_q_heads, w.num_kv_splits, dev, torch.float16)
     times = []
@@ -186,8 +189,9 @@ def full_decode_time(dev, flush, timer, reps=30):
             times.append(timer.elapsed_ms(a, b) * 1e3)
         timer.destroy(a, b)
     us = statistics.median(times)
-    nbytes = (int(w.seq_lens.sum()) * w.num_kv_heads * 134 + w.query.nbytes + w.query.nbytes
-              + w.batch * w.num_q_heads * 4 + w.block_table.nbytes)
+    rows = w.batch * w.num_q_heads
+    nbytes = (int(w.seq_lens.sum()) * w.num_kv_heads * 134 + rows * w.head_dim * 2 * 2 + rows * 4
+              + w.block_table.nbytes + w.rotation_t.nbytes)
     return {"workload": "b256_ctx2048_32q8kv_s16_fp16", "us": round(us, 2),
             "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes}
 
@@ -236,6 +240,34 @@ def cpu_baseline_c(w, threads: int, repeats: int = 3):
             "sample": "whole workload, C oracle tq4o_stage1 (OpenMP), median of %d" % repeats}
 
 
+def side_workload(args, dev) -> int:
+    """One JSON line for a workload beside the headline (the writer or the full step)."""
+    import torch
+
+    flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
+    timer = HipEvents(torch.cuda.current_stream(dev).cuda_stream)
+    if args.workload.startswith("store_"):
+        size = args.workload[len("store_"):]
+        r = store_times(dev, flush, timer, reps=args.steps, only=size)
+        us, gbs = r[f"{size}_us"], r[f"{size}_GBps"]
+        metric = f"cache writer (tq4_store, SoA, bf16 K/V, 8 kv-heads) {size}: GB/s"
+        timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
+        dtype = "bf16 in, f32 math"
+    else:
+        r = full_decode_time(dev, flush, timer, reps=args.steps)
+        us, gbs = r["us"], r["GBps"]
+        metric = "full decode step B256 x ctx2048 (rotation + Stage1 + Stage2): GB/s"
+        timing = "events recorded around the step, median"
+        dtype = "fp16 in/out, f32 math"
+    print(json.dumps({"metric": metric, "value": gbs, "unit": "GB/s", "n_gpus": 1,
+                      "steps": args.steps, "ms_per_step": round(us / 1e3, 5),
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                      "dtype": dtype, "data": "synthetic",
+                      "config": {"workload": args.workload}, "timing": timing,
+                      "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,6 +279,10 @@ def main() -> int:
     ap.add_argument("--no-variants", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (PMC byte-counter calibration)")
+    ap.add_argument("--workload", default="stage1",
+                    choices=["stage1", "store_decode_b64", "store_prefill_n8192", "full_decode_b256"],
+                    help="stage1: the headline (default); the others time only that workload "
+                         "(--steps cold launches) and print its own JSON line, e.g. for a profile")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -260,6 +296,8 @@ def main() -> int:
     from tq4_decode import ops, workloads
 
     dev = torch.device("cuda:0")
+    if args.workload != "stage1":
+        return side_workload(args, dev)
     w = workloads.qwen3_4b_b64_ctx4096()
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     q, bt, sl, lut = t(w.q_rot), t(w.block_table), t(w.seq_lens), t(w.pair_lut)
