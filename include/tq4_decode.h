@@ -128,6 +128,30 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
               uint8_t *kv_cache, int N, int Hk, int D, int block_size,
               int64_t cache_block_stride, int layout, int norm_correction, tq4_stream_t stream);
 
+/*
+ * FP8-key preset (turboquant_k8v4): Stage1 over a cache whose K is one OCP E4M3 byte per
+ * dim (record 128 K bytes | 64 V bytes, SoA metadata fields V scale and V zero; AoS slot
+ * 196 bytes = K | V | scale | zero).  query is the unrotated query (fp32 [B, Hq, D]);
+ * score = q.k * attn_scale.  Same mid_o contract, grid rule and sinks as tq4_stage1_ex;
+ * runs on the VALU kernel.
+ * Replaces: _tq_decode_stage1 with KEY_FP8=1, reference/soa_decode_v1.py:213-230 (launch
+ *           :519-606); the AoS kernel reference/aos_decode.py.
+ */
+int tq4_stage1_fp8(const float *query, const uint8_t *kv_cache, const int32_t *block_table,
+                   const int32_t *seq_lens, float *mid_o, int B, int Hq, int Hk, int D, int block_size,
+                   int max_blocks_per_seq, int64_t cache_block_stride, int num_kv_splits, int layout,
+                   float attn_scale, const float *sinks, tq4_stream_t stream);
+
+/*
+ * FP8-key preset writer: K cast to E4M3 (round to nearest even, saturating at +-448, NaN
+ * kept), V as tq4_store; layout TQ4_LAYOUT_SOA or TQ4_LAYOUT_AOS; slots < 0 skipped.
+ * Replaces: _tq_fused_store_fp8 reference/soa_store.py:125-212 (launch :446-478) and the
+ *           AoS FP8 store of reference/aos_store.py.
+ */
+int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
+                  uint8_t *kv_cache, int N, int Hk, int D, int block_size, int64_t cache_block_stride,
+                  int layout, tq4_stream_t stream);
+
 /* Message of the last failed call on this thread ("" when none).
  * Replaces: the TORCH_CHECK messages of cuda/tq4_cuda_v1.cu:468-499. */
 const char *tq4_last_error(void);

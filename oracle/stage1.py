@@ -53,12 +53,23 @@ def decode_kv(cache, blocks, offs, kvh, centroids, is_aos, block_size, num_kv_he
     return k, v
 
 
+def decode_kv_fp8(cache, blocks, offs, kvh, is_aos, block_size, num_kv_heads, head_dim):
+    """FP8-key preset: float64 ``(K [T, D], V [T, D])``; K is the E4M3 value of each byte
+    (``reference/soa_decode_v1.py:213-230`` with KEY_FP8), no norm."""
+    from . import fp8
+
+    kb, v_code, v_scale, v_zero = fp8.gather(cache, blocks, offs, kvh, block_size, num_kv_heads,
+                                            head_dim, is_aos)
+    return fp8.decode(kb), v_code.astype(np.float64) * v_scale[:, None] + v_zero[:, None]
+
+
 def stage1(q_rot, cache, block_table, seq_lens, centroids, num_splits, *, num_kv_heads,
-           block_size=16, is_aos=False, attn_scale=None, mid_o=None, sinks=None):
+           block_size=16, is_aos=False, attn_scale=None, mid_o=None, sinks=None, key_fp8=False):
     """Return ``mid_o`` float64 ``[B, Hq, S, D+1]``; empty splits keep their prior value
     (NaN when ``mid_o`` is not given).  ``sinks`` ``[Hq]``: split 0 of every sequence starts
     its softmax with max = sink and sum = 1, an extra logit with a zero value
-    (``reference/soa_decode_v1.py:134-148``)."""
+    (``reference/soa_decode_v1.py:134-148``).  ``key_fp8``: the FP8-key preset; ``q_rot``
+    is then the unrotated query and ``centroids`` is unused."""
     q = np.asarray(q_rot, dtype=np.float64)
     batch, num_q_heads, head_dim = q.shape
     group = num_q_heads // num_kv_heads
@@ -76,8 +87,12 @@ def stage1(q_rot, cache, block_table, seq_lens, centroids, num_splits, *, num_kv
             blocks = bt[b, tok // block_size]
             offs = tok % block_size
             for kvh in range(num_kv_heads):
-                k, v = decode_kv(cache, blocks, offs, kvh, centroids, is_aos,
-                                 block_size, num_kv_heads, head_dim)
+                if key_fp8:
+                    k, v = decode_kv_fp8(cache, blocks, offs, kvh, is_aos, block_size,
+                                         num_kv_heads, head_dim)
+                else:
+                    k, v = decode_kv(cache, blocks, offs, kvh, centroids, is_aos,
+                                     block_size, num_kv_heads, head_dim)
                 heads = slice(kvh * group, (kvh + 1) * group)
                 s = (q[b, heads] @ k.T) * scale
                 m = s.max(axis=1, keepdims=True)

@@ -102,3 +102,37 @@ def store(key, value, slot_mapping, rot_t, cents, cache, *, block_size=16, is_ao
             _put_fp16(flat, fld(layout.SOA_V_SCALE), scale[sel, h])
             _put_fp16(flat, fld(layout.SOA_V_ZERO), vmin[sel, h])
     return cache
+
+
+def store_fp8(key, value, slot_mapping, cache, *, block_size=16, is_aos=False):
+    """FP8-key preset writer (``reference/soa_store.py:125-212``; AoS ``reference/aos_store.py``):
+    K bytes = E4M3 of the raw key (saturating), V as ``quantize_values``."""
+    from . import fp8
+
+    n_tok, num_kv_heads, head_dim = np.asarray(key).shape
+    flat = cache.reshape(-1)
+    kbytes = fp8.encode(np.asarray(key, dtype=np.float32))
+    codes, scale, vmin = quantize_values(value)
+    vbytes = pack_nibbles(codes)
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    sel = np.nonzero(slots >= 0)[0]
+    b, t = slots[sel] // block_size, slots[sel] % block_size
+    stride = fp8.block_bytes(block_size, num_kv_heads, head_dim)
+    rec = fp8.record_bytes(head_dim)
+    kcols = np.arange(head_dim, dtype=np.int64)
+    vcols = np.arange(head_dim // 2, dtype=np.int64)
+    for h in range(num_kv_heads):
+        if is_aos:
+            slot = fp8.slot_bytes(head_dim)
+            base = b * stride + t * (num_kv_heads * slot) + h * slot
+            _put_fp16(flat, base + rec, scale[sel, h])
+            _put_fp16(flat, base + rec + 2, vmin[sel, h])
+        else:
+            base = b * stride + t * (num_kv_heads * rec) + h * rec
+            meta = b * stride + block_size * num_kv_heads * rec
+            fld = lambda f: meta + ((h * fp8.NUM_SOA_FIELDS + f) * block_size + t) * 2  # noqa: E731
+            _put_fp16(flat, fld(fp8.SOA_V_SCALE), scale[sel, h])
+            _put_fp16(flat, fld(fp8.SOA_V_ZERO), vmin[sel, h])
+        flat[base[:, None] + kcols[None, :]] = kbytes[sel, h]
+        flat[base[:, None] + head_dim + vcols[None, :]] = vbytes[sel, h]
+    return cache

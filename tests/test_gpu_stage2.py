@@ -140,10 +140,10 @@ def test_backend_decode_entry(dev, layout):
     print(f"{layout} decode entry fp16 max-abs {err:.3e}")
     assert err <= 1e-3
     assert np.abs(lse_buf[:5].cpu().numpy()[live] - rl[live]).max() <= 1e-4
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError):  # 3-bit keys are not built
         mod.triton_turboquant_decode_attention(
             t(query), t(cache), t(w.block_table), t(w.seq_lens), t(rot_t.T.copy()), t(w.centroids),
-            128 ** -0.5, mse_bits=4, key_packed_size=66, value_quant_bits=4, key_fp8=True)
+            128 ** -0.5, mse_bits=3, key_packed_size=50, value_quant_bits=4)
     # with sinks (split 0 starts from the head's sink logit)
     sinks = rng.normal(0.0, 2.0, 32).astype(np.float32)
     out = mod.triton_turboquant_decode_attention(

@@ -16,7 +16,10 @@
 
 namespace tq4 {
 
-template <int LAYOUT, int G>
+// KF8: the FP8-key preset -- K is one E4M3 byte per dim (no codebook, no norm, the query
+// is not rotated); record D + D/2 bytes (SoA; two metadata fields: V scale, V zero) or a
+// D + D/2 + 4 byte slot (AoS: V scale and zero after the V codes).
+template <int LAYOUT, int G, bool KF8 = false>
 __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
@@ -36,7 +39,7 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
     __shared__ float pw[G][kWave];
     __shared__ uint32_t vstage[kWave][kHalfD / 4 + 1];  // +1 word: bank spread
 
-    if (lane < 16)
+    if (!KF8 && lane < 16)
         lut[lane] = pair_lut[2 * (lane * 16)];  // row (lane, 0) = (c[lane], c[0])
     for (int i = lane; i < G * kHeadDim; i += kWave) {
         const int h = i / kHeadDim, d = i % kHeadDim;
@@ -64,7 +67,22 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
         const int off = tc % block_size;
         const uint8_t *kp, *vp;
         float norm, vscale, vzero;
-        if (LAYOUT == 0) {
+        if constexpr (KF8) {
+            constexpr int rec = kHeadDim + kHalfD;
+            if (LAYOUT == 0) {
+                kp = cache + blk * block_stride + ((int64_t)off * num_kv_heads + kvh) * rec;
+                const uint8_t *meta = cache + blk * block_stride + (int64_t)block_size * num_kv_heads * rec +
+                                      ((int64_t)kvh * 2 * block_size + off) * 2;
+                vscale = load_half(meta);
+                vzero = load_half(meta + 2 * block_size);
+            } else {
+                kp = cache + blk * block_stride + ((int64_t)off * num_kv_heads + kvh) * (rec + 4);
+                vscale = load_half(kp + rec);
+                vzero = load_half(kp + rec + 2);
+            }
+            vp = kp + kHeadDim;
+            norm = 1.f;
+        } else if (LAYOUT == 0) {
             kp = soa_record(cache, blk, block_stride, off, num_kv_heads, kvh);
             vp = kp + kHalfD;
             norm = load_half(soa_meta(cache, blk, block_stride, off, num_kv_heads, kvh, block_size, 0));
@@ -83,21 +101,37 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
         for (int h = 0; h < G; ++h)
             s[h] = 0.f;
         float csq = 0.f;
-        for (int w = 0; w < kHalfD / 4; ++w) {
-            const uint32_t word = load_u32_a2(kp + 4 * w);
+        if constexpr (KF8) {
+            for (int w = 0; w < kHeadDim / 4; ++w) {
+                const uint32_t word = load_u32_a2(kp + 4 * w);
+                const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
+                const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
+                const float k4[4] = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                const float c = lut[(word >> (4 * n)) & 15u];
-                if (LAYOUT == 1)
-                    csq += c * c;
+                for (int n = 0; n < 4; ++n)
 #pragma unroll
-                for (int h = 0; h < G; ++h)
-                    s[h] += qs[h][8 * w + n] * c;
+                    for (int h = 0; h < G; ++h)
+                        s[h] += qs[h][4 * w + n] * k4[n];
             }
-            vstage[lane][w] = load_u32_a2(vp + 4 * w);
+            for (int w = 0; w < kHalfD / 4; ++w)
+                vstage[lane][w] = load_u32_a2(vp + 4 * w);
+        } else {
+            for (int w = 0; w < kHalfD / 4; ++w) {
+                const uint32_t word = load_u32_a2(kp + 4 * w);
+#pragma unroll
+                for (int n = 0; n < 8; ++n) {
+                    const float c = lut[(word >> (4 * n)) & 15u];
+                    if (LAYOUT == 1)
+                        csq += c * c;
+#pragma unroll
+                    for (int h = 0; h < G; ++h)
+                        s[h] += qs[h][8 * w + n] * c;
+                }
+                vstage[lane][w] = load_u32_a2(vp + 4 * w);
+            }
         }
         float kscale = norm;
-        if (LAYOUT == 1)
+        if (!KF8 && LAYOUT == 1)
             kscale = norm * (1.0f / sqrtf(csq + 1e-16f));
 
 #pragma unroll

@@ -126,6 +126,39 @@ __device__ __forceinline__ void store16_a2(uint8_t *p, uint4 v) {
     }
 }
 
+// V of one row chunk (the lane's 32 dims; the row's four lanes n + 16g reduce together):
+// scale = max((max - min) / 15, 1e-8), code = clamp(int((v - min) / scale + 0.5), 0, 15),
+// packed two per byte (element j at bits 4(j % 8) of word j / 8).  The product with the
+// reciprocal is within 2^-18 of the fp32 quotient for quotients below 16, so the code only
+// differs when quotient + 0.5 lies within 2^-16 of an integer: those elements take the
+// division.
+__device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[4], float &scale, float &vmin) {
+    float lo = x[0], hi = x[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) {
+        lo = fminf(lo, x[i]);
+        hi = fmaxf(hi, x[i]);
+    }
+    vmin = row_min(lo);
+    const float vmax = row_max(hi);
+    scale = (vmax - vmin) / 15.0f;
+    scale = scale > 1e-8f ? scale : 1e-8f;
+    const float rs = 1.f / scale;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        vw[q] = 0u;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        float f = (x[j] - vmin) * rs + 0.5f;
+        if (fabsf(f - rintf(f)) < 0x1p-16f) {  // near a code boundary: the division
+            asm volatile("");                   // (keeps it behind the branch)
+            f = (x[j] - vmin) / scale + 0.5f;
+        }
+        const int c = (int)f;
+        vw[j / 8] |= (uint32_t)(c < 0 ? 0 : (c > 15 ? 15 : c)) << (4 * (j % 8));
+    }
+}
+
 template <int LAYOUT, class T>
 __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4))) void store_kernel(
     const T *__restrict__ key, const T *__restrict__ value, const int32_t *__restrict__ slot_mapping,
@@ -291,27 +324,9 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
         if constexpr (!kEarlyV)
             load_raw(vr, value + (int64_t)row * kHeadDim + 32 * g, in_range);
         to_floats(x, vr);
-        float lo = x[0], hi = x[0];
-#pragma unroll
-        for (int i = 1; i < 32; ++i) {
-            lo = fminf(lo, x[i]);
-            hi = fmaxf(hi, x[i]);
-        }
-        const float vmin = row_min(lo), vmax = row_max(hi);
-        float scale = (vmax - vmin) / 15.0f;
-        scale = scale > 1e-8f ? scale : 1e-8f;
-        const float rs = 1.f / scale;
-        uint32_t vw[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            float f = (x[j] - vmin) * rs + 0.5f;
-            if (fabsf(f - rintf(f)) < 0x1p-16f) {  // near a code boundary: the division
-                asm volatile("");                   // (keeps it behind the branch)
-                f = (x[j] - vmin) / scale + 0.5f;
-            }
-            const int c = (int)f;
-            vw[j / 8] |= (uint32_t)(c < 0 ? 0 : (c > 15 ? 15 : c)) << (4 * (j % 8));
-        }
+        float scale, vmin;
+        uint32_t vw[4];
+        quantize_v(x, vw, scale, vmin);
 
         const int slot = in_range ? slot_mapping[tok] : -1;
         if (slot >= 0) {
@@ -344,6 +359,77 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
         load_raw(kr, key + nrow * kHeadDim + 32 * g, nrow < rows);
         if constexpr (kEarlyV)
             load_raw(vr, value + nrow * kHeadDim + 32 * g, nrow < rows);
+    }
+}
+
+// FP8-key preset writer (reference/soa_store.py:125-212): K cast to E4M3 bytes (round to
+// nearest even, saturating at +-448 as the reference's satfinite cast; NaN stays NaN), V as
+// above.  SoA record (t, h) = 128 K bytes | 64 V bytes, metadata [h][field][t] with two
+// fields (V scale, V zero); AoS slot = 128 K | 64 V | scale | zero (196 bytes, 4-byte
+// aligned: dword stores).  A wave takes 16 rows; lane (n, g) = row n, dims 32g .. 32g+31.
+constexpr int kFp8Waves = 4;
+constexpr int kFp8Record = kHeadDim + kHalfD;
+__device__ __forceinline__ float sat_e4m3(float x) {
+    return x > 448.f ? 448.f : (x < -448.f ? -448.f : x);  // comparisons keep NaN
+}
+template <int LAYOUT, class T>
+__global__ __launch_bounds__(kWave *kFp8Waves) void store_fp8_kernel(const T *__restrict__ key,
+                                                                     const T *__restrict__ value,
+                                                                     const int32_t *__restrict__ slot_mapping,
+                                                                     uint8_t *__restrict__ cache, int rows,
+                                                                     int num_kv_heads, int block_size,
+                                                                     int64_t block_stride) {
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int n = lane & 15, g = lane >> 4;
+    const int tiles = (rows + kRows - 1) / kRows;
+    for (int tile = blockIdx.x * kFp8Waves + wave; tile < tiles; tile += gridDim.x * kFp8Waves) {
+        const int row = tile * kRows + n;
+        const bool in_range = row < rows;
+        Chunk<T> kr, vr;
+        load_raw(kr, key + (int64_t)row * kHeadDim + 32 * g, in_range);
+        load_raw(vr, value + (int64_t)row * kHeadDim + 32 * g, in_range);
+        float x[32];
+        to_floats(x, kr);
+        uint32_t kw[8];  // dims 32g + 4i .. 32g + 4i + 3, low byte first
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int p = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(x[4 * i]), sat_e4m3(x[4 * i + 1]), 0, false);
+            p = __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(x[4 * i + 2]), sat_e4m3(x[4 * i + 3]), p, true);
+            kw[i] = (uint32_t)p;
+        }
+        to_floats(x, vr);
+        float scale, vmin;
+        uint32_t vw[4];
+        quantize_v(x, vw, scale, vmin);
+        const int tok = in_range ? row / num_kv_heads : 0;
+        const int head = in_range ? row % num_kv_heads : 0;
+        const int slot = in_range ? slot_mapping[tok] : -1;
+        if (slot < 0)
+            continue;
+        const int64_t blk = slot / block_size, off = slot % block_size;
+        uint8_t *base = cache + blk * block_stride;
+        const int rec = LAYOUT == 0 ? kFp8Record : kFp8Record + 4;
+        uint32_t *r = reinterpret_cast<uint32_t *>(base + (off * num_kv_heads + head) * rec);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            r[8 * g + i] = kw[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            r[kHeadDim / 4 + 4 * g + i] = vw[i];
+        if (g == 0) {
+            uint16_t *f;
+            int fstride;
+            if constexpr (LAYOUT == 0) {
+                f = reinterpret_cast<uint16_t *>(base + (int64_t)block_size * num_kv_heads * kFp8Record) +
+                    (int64_t)head * 2 * block_size + off;
+                fstride = block_size;
+            } else {
+                f = reinterpret_cast<uint16_t *>(reinterpret_cast<uint8_t *>(r) + kFp8Record);
+                fstride = 1;
+            }
+            f[0] = half_bits(scale);
+            f[fstride] = half_bits(vmin);
+        }
     }
 }
 

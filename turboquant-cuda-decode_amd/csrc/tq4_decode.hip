@@ -86,12 +86,13 @@ struct Stage1Args {
     void *out = nullptr;
     int out_dtype = TQ4_F32;
     float *lse = nullptr;
+    bool key_fp8 = false;  // the FP8-key preset (VALU kernel; pair LUT unused)
 };
 static_assert(tq4::kOutF32 == TQ4_F32 && tq4::kOutBf16 == TQ4_BF16 && tq4::kOutF16 == TQ4_F16,
               "output type ids");
 
 int check_stage1(const Stage1Args &a) {
-    if (!a.q_rot || !a.cache || !a.bt || !a.seq_lens || !a.lut || !a.mid_o)
+    if (!a.q_rot || !a.cache || !a.bt || !a.seq_lens || (!a.lut && !a.key_fp8) || !a.mid_o)
         return fail(TQ4_E_INVALID, "tq4_stage1: null pointer argument");
     if (a.B <= 0 || a.Hq <= 0 || a.Hk <= 0 || a.S <= 0 || a.bs <= 0 || a.max_blocks <= 0)
         return fail(TQ4_E_INVALID, "tq4_stage1: B, Hq, Hk, num_kv_splits, block_size and "
@@ -102,10 +103,11 @@ int check_stage1(const Stage1Args &a) {
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: head_dim %d unsupported (kernels are built for 128)", a.D);
     if (a.layout != TQ4_LAYOUT_SOA && a.layout != TQ4_LAYOUT_AOS)
         return fail(TQ4_E_INVALID, "tq4_stage1: layout must be 0 (SoA) or 1 (AoS)");
-    const int64_t min_stride = (int64_t)a.bs * a.Hk * tq4::kAosSlot;
+    const int slot = a.key_fp8 ? tq4::store::kFp8Record + 4 : tq4::kAosSlot;
+    const int64_t min_stride = (int64_t)a.bs * a.Hk * slot;
     if (a.stride < min_stride || a.stride % 2)
-        return fail(TQ4_E_INVALID, "tq4_stage1: requires cache [blocks,%d,%d,134]: block stride %lld < %lld",
-                    a.bs, a.Hk, (long long)a.stride, (long long)min_stride);
+        return fail(TQ4_E_INVALID, "tq4_stage1: requires cache [blocks,%d,%d,%d]: block stride %lld < %lld",
+                    a.bs, a.Hk, slot, (long long)a.stride, (long long)min_stride);
     if (!aligned(a.cache, 16) || !aligned(a.q_rot, 16) || !aligned(a.mid_o, 4))
         return fail(TQ4_E_INVALID, "tq4_stage1: kv_cache and q_rot must be 16-byte aligned");
     if (!(a.scale > 0.f) || a.scale != a.scale)
@@ -115,7 +117,9 @@ int check_stage1(const Stage1Args &a) {
 
 template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t st) {
     const dim3 grid(a.S, a.Hk, a.B);
-    launch(&tq4::stage1_simple_kernel<LAYOUT, G>, grid, dim3(tq4::kWave), st,
+    const auto kernel = a.key_fp8 ? &tq4::stage1_simple_kernel<LAYOUT, G, true>
+                                  : &tq4::stage1_simple_kernel<LAYOUT, G, false>;
+    launch(kernel, grid, dim3(tq4::kWave), st,
                        a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.sinks, a.Hq, a.Hk, a.bs,
                        a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
@@ -251,8 +255,11 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     if (rc)
         return rc;
     // AUTO: the 16x16x32 kernel wherever the MFMA kernels apply (both layouts), else VALU.
+    // The FP8-key preset runs on the VALU kernel.
+    if (a.key_fp8 && kernel != TQ4_KERNEL_AUTO && kernel != TQ4_KERNEL_SIMPLE)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: FP8 keys run on the VALU kernel");
     if (kernel == TQ4_KERNEL_AUTO)
-        kernel = mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE;
+        kernel = a.key_fp8 ? TQ4_KERNEL_SIMPLE : (mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE);
     if (kernel == TQ4_KERNEL_MFMA && a.sinks)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_ex: sinks need the XDL or the VALU kernel");
     if (kernel == TQ4_KERNEL_MFMA)
@@ -327,6 +334,17 @@ int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block
     return tq4_stage1_ex(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o, B, Hq, Hk, D,
                          block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits,
                          layout, attn_scale, TQ4_KERNEL_AUTO, nullptr, stream);
+}
+
+int tq4_stage1_fp8(const float *query, const uint8_t *kv_cache, const int32_t *block_table,
+                   const int32_t *seq_lens, float *mid_o, int B, int Hq, int Hk, int D, int block_size,
+                   int max_blocks_per_seq, int64_t cache_block_stride, int num_kv_splits, int layout,
+                   float attn_scale, const float *sinks, tq4_stream_t stream) {
+    Stage1Args a{query, kv_cache, block_table, seq_lens, nullptr, mid_o, B, Hq, Hk, D,
+                 block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
+                 attn_scale, sinks};
+    a.key_fp8 = true;
+    return run_stage1(a, TQ4_KERNEL_SIMPLE, reinterpret_cast<hipStream_t>(stream));
 }
 
 int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_dtype,
@@ -461,6 +479,51 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
     }
 #undef TQ4_STORE_LAUNCH
     return launch_status("store");
+}
+
+int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
+                  uint8_t *kv_cache, int N, int Hk, int D, int block_size, int64_t cache_block_stride,
+                  int layout, tq4_stream_t stream) {
+    if (!key || !value || !slot_mapping || !kv_cache)
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: null pointer argument");
+    if (N < 0 || Hk <= 0 || block_size <= 0)
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: N must be >= 0, Hk and block_size positive");
+    if (D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_store_fp8: head_dim %d unsupported (128)", D);
+    if (layout != TQ4_LAYOUT_SOA && layout != TQ4_LAYOUT_AOS)
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: layout must be 0 (SoA) or 1 (AoS)");
+    const int slot = tq4::store::kFp8Record + 4;
+    const int64_t min_stride = (int64_t)block_size * Hk * slot;
+    if (cache_block_stride < min_stride || cache_block_stride % 4)
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: requires cache [blocks,%d,%d,%d]: block stride %lld",
+                    block_size, Hk, slot, (long long)cache_block_stride);
+    if (!aligned(key, 16) || !aligned(value, 16) || !aligned(kv_cache, 4))
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: key and value must be 16-byte aligned, kv_cache 4-byte");
+    if ((int64_t)N * Hk > INT32_MAX - 64)
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: N * Hk = %lld rows exceeds the 32-bit row index",
+                    (long long)N * Hk);
+    if (N == 0)
+        return ok();
+    const int rows = N * Hk;
+    const int per_group = tq4::store::kRows * tq4::store::kFp8Waves;
+    const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, 2048));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define TQ4_STORE_FP8_LAUNCH(L, T)                                                                   \
+    launch(&tq4::store::store_fp8_kernel<L, T>, grid, dim3(tq4::kWave * tq4::store::kFp8Waves), st, \
+           static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, kv_cache, rows, Hk,  \
+           block_size, cache_block_stride)
+    switch (dtype * 2 + layout) {
+    case TQ4_F32 * 2 + 0: TQ4_STORE_FP8_LAUNCH(0, float); break;
+    case TQ4_F32 * 2 + 1: TQ4_STORE_FP8_LAUNCH(1, float); break;
+    case TQ4_BF16 * 2 + 0: TQ4_STORE_FP8_LAUNCH(0, __bf16); break;
+    case TQ4_BF16 * 2 + 1: TQ4_STORE_FP8_LAUNCH(1, __bf16); break;
+    case TQ4_F16 * 2 + 0: TQ4_STORE_FP8_LAUNCH(0, _Float16); break;
+    case TQ4_F16 * 2 + 1: TQ4_STORE_FP8_LAUNCH(1, _Float16); break;
+    default:
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
+    }
+#undef TQ4_STORE_FP8_LAUNCH
+    return launch_status("store_fp8");
 }
 
 }  // extern "C"

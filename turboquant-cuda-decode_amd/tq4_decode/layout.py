@@ -31,6 +31,13 @@ def slot_bytes(head_dim: int) -> int:
     return raw + raw % 2
 
 
+def slot_bytes_fp8(head_dim: int) -> int:
+    """FP8-key preset slot: one E4M3 byte per K dim + V codes + fp16 V scale and zero
+    (``reference/config.py:128-164``)."""
+    raw = head_dim + head_dim // 2 + 4
+    return raw + raw % 2
+
+
 def block_bytes(block_size: int, num_kv_heads: int, head_dim: int) -> int:
     return block_size * num_kv_heads * slot_bytes(head_dim)
 

@@ -27,7 +27,7 @@ import torch
 
 from . import _lib
 from ._lib import Tq4Error  # noqa: F401  (raised by every wrapper)
-from .layout import AOS, LAYOUTS, SOA, slot_bytes
+from .layout import AOS, LAYOUTS, SOA, slot_bytes, slot_bytes_fp8
 
 KERNELS = {"auto": 0, "simple": 1, "mfma": 2, "xdl": 3}
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -199,6 +199,62 @@ def store(key, value, kv_cache, slot_mapping, rotation_t, midpoints, centroids=N
     return kv_cache
 
 
+def stage1_fp8(query, kv_cache, block_table, seq_lens, mid_o=None, *, num_kv_splits=None,
+               layout="soa", attn_scale=None, sinks=None):
+    """Stage1 of the FP8-key preset (``turboquant_k8v4``): ``query`` fp32 ``[B, Hq, D]``
+    (not rotated), K one E4M3 byte per dim; returns ``mid_o [B, Hq, S, D+1]``."""
+    for t, n, dt in ((query, "query", torch.float32), (kv_cache, "kv_cache", torch.uint8),
+                     (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32)):
+        _check_tensor(t, n, dt)
+    _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
+    B, Hq, D = query.shape
+    _require(kv_cache.dim() == 4, "kv_cache must be [blocks, block_size, Hk, slot]")
+    _, bs, Hk, slot = kv_cache.shape
+    _require(slot == slot_bytes_fp8(D), f"requires slot_size={slot_bytes_fp8(D)} (FP8 keys)")
+    _require(Hq % Hk == 0, "Hq must be a multiple of Hk")
+    _require(block_table.dim() == 2 and block_table.size(0) == B, "block_table batch mismatch")
+    _require(seq_lens.dim() == 1 and seq_lens.size(0) == B, "seq_lens batch mismatch")
+    if mid_o is None:
+        _require(num_kv_splits is not None and num_kv_splits > 0,
+                 "num_kv_splits is required when mid_o is None")
+        mid_o = torch.empty(B, Hq, num_kv_splits, D + 1, dtype=torch.float32, device=query.device)
+    _check_tensor(mid_o, "mid_o", torch.float32)
+    S = mid_o.size(2)
+    _require(tuple(mid_o.shape) == (B, Hq, S, D + 1), f"mid_o must be [B,{Hq},S,{D + 1}]")
+    devs = {t.device for t in (query, kv_cache, block_table, seq_lens, mid_o)}
+    _require(len(devs) == 1, "all tensors must be on the same device")
+    scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
+    rc = _lib.load().tq4_stage1_fp8(
+        query.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
+        mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), kv_cache.stride(0), S,
+        _layout_id(layout), scale, _check_sinks(sinks, Hq, query.device), _stream(query.device))
+    _lib.check(rc, "tq4_stage1_fp8")
+    return mid_o
+
+
+def store_fp8(key, value, kv_cache, slot_mapping, *, layout="soa"):
+    """Writer of the FP8-key preset: K cast to E4M3 (round to nearest even, saturating at
+    +-448), V 4-bit uniform; returns ``kv_cache``."""
+    _require(key.is_cuda and key.dtype in DTYPES and key.is_contiguous(), "invalid key")
+    _require(value.dtype == key.dtype and value.is_contiguous() and value.shape == key.shape,
+             "value must match key (shape, dtype, contiguous)")
+    _require(key.dim() == 3 and key.size(2) == HEAD_DIM, f"key must be [N, Hk, {HEAD_DIM}]")
+    _check_tensor(kv_cache, "kv_cache", torch.uint8)
+    _check_tensor(slot_mapping, "slot_mapping", torch.int32)
+    N, Hk, D = key.shape
+    _require(kv_cache.dim() == 4 and kv_cache.size(2) == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
+    _require(kv_cache.size(3) == slot_bytes_fp8(D), f"requires slot_size={slot_bytes_fp8(D)} (FP8 keys)")
+    _require(slot_mapping.numel() == N, "slot_mapping must have one entry per token")
+    devs = {t.device for t in (key, value, kv_cache, slot_mapping)}
+    _require(len(devs) == 1, "all tensors must be on the same device")
+    rc = _lib.load().tq4_store_fp8(
+        key.data_ptr(), value.data_ptr(), DTYPES[key.dtype], slot_mapping.data_ptr(),
+        kv_cache.data_ptr(), N, Hk, D, kv_cache.size(1), kv_cache.stride(0), _layout_id(layout),
+        _stream(key.device))
+    _lib.check(rc, "tq4_store_fp8")
+    return kv_cache
+
+
 class DecodeWorkspace:
     """Preallocated buffers of one full decode step (fixed shapes, reusable)."""
 
@@ -266,12 +322,16 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
     Caller buffers are used when they fit (``mid_o_buf`` fp32 ``[>=B, Hq, S, D+1]``,
     ``output_buf`` ``[>=B, Hq, D]`` in the query dtype, ``lse_buf`` fp32 ``[>=B, Hq]``); the
     rotated query and the pair LUT live on ``buf_holder`` when one is given; ``sinks``
-    (fp32 ``[Hq]``) enter split 0.  Built for the 4-bit ``turboquant_4bit_nc`` cache: FP8
-    keys, other bit widths and AoS without norm correction raise ``NotImplementedError``.
+    (fp32 ``[Hq]``) enter split 0.  Built for the 4-bit ``turboquant_4bit_nc`` cache and,
+    with ``key_fp8``, the ``turboquant_k8v4`` cache (unrotated query, VALU Stage1); other
+    bit widths and 4-bit AoS without norm correction raise ``NotImplementedError``.
     """
+    _require(value_quant_bits == 4, "only 4-bit values are built")
     if key_fp8:
-        raise NotImplementedError("FP8 keys (the k8v4 presets) are not built")
-    _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
+        return _decode_attention_fp8(query, kv_cache, block_table, seq_lens, scale, key_packed_size,
+                                     mid_o_buf, output_buf, lse_buf, buf_holder, max_num_kv_splits,
+                                     sinks, layout)
+    _require(mse_bits == 4, "only 4-bit MSE keys are built")
     _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
     if layout == "aos" and not norm_correction:
         raise NotImplementedError("AoS decode is built with the norm correction (turboquant_4bit_nc)")
@@ -309,6 +369,30 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
     return out
 
 
+def _decode_attention_fp8(query, kv_cache, block_table, seq_lens, scale, key_packed_size,
+                          mid_o_buf, output_buf, lse_buf, buf_holder, max_num_kv_splits, sinks,
+                          layout):
+    """FP8-key decode (``reference/soa_decode_v1.py:528-534`` passes the query unrotated)."""
+    _require(key_packed_size == HEAD_DIM, f"key_packed_size must be {HEAD_DIM} for FP8 keys")
+    B, Hq, D = query.shape
+    S = int(max_num_kv_splits)
+    mid_o = _buffer_view(mid_o_buf, (B, Hq, S, D + 1), torch.float32)
+    if mid_o is None:
+        mid_o = torch.empty(B, Hq, S, D + 1, dtype=torch.float32, device=query.device)
+        if buf_holder is not None:
+            buf_holder._tq_mid_o_buf = mid_o
+    out = _buffer_view(output_buf, (B, Hq, D), query.dtype)
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=query.dtype, device=query.device)
+    lse = _buffer_view(lse_buf, (B, Hq), torch.float32)
+    if lse is None:
+        lse = torch.empty(B, Hq, dtype=torch.float32, device=query.device)
+    stage1_fp8(query.float().contiguous(), kv_cache, block_table, seq_lens, mid_o, layout=layout,
+               attn_scale=scale, sinks=sinks)
+    stage2(mid_o, seq_lens, out, lse, out_dtype=query.dtype)
+    return out
+
+
 # ---- reference harness call shapes -------------------------------------------------
 
 def launch_tq4_v2_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, pair_lut, mid_o=None,
@@ -342,8 +426,11 @@ def triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, 
                             norm_correction=False):
     """SoA cache writer with the ``reference/soa_store.py:381-397`` signature (MSE path,
     4-bit keys and values; the FP8-key path and other bit widths are not built)."""
-    if key_fp8:
-        raise NotImplementedError("FP8 keys (the k8v4 presets) are not built")
+    if key_fp8:  # turboquant_k8v4: no rotation, no codebook
+        _require(value_quant_bits == 4 and key_packed_size == HEAD_DIM, "FP8 keys need 4-bit values "
+                 f"and key_packed_size {HEAD_DIM}")
+        store_fp8(key, value, kv_cache, slot_mapping, layout="soa")
+        return
     _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
     _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
     store(key, value, kv_cache, slot_mapping, PiT, midpoints, centroids, layout="soa",
@@ -354,8 +441,11 @@ def aos_triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoin
                                 key_packed_size, value_quant_bits, key_fp8=False):
     """AoS cache writer with the ``reference/aos_store.py:350-361`` signature (MSE path,
     4-bit keys and values; the slot keeps the raw fp16 norm, no norm correction)."""
-    if key_fp8:
-        raise NotImplementedError("FP8 keys (the k8v4 presets) are not built")
+    if key_fp8:  # turboquant_k8v4: no rotation, no codebook
+        _require(value_quant_bits == 4 and key_packed_size == HEAD_DIM, "FP8 keys need 4-bit values "
+                 f"and key_packed_size {HEAD_DIM}")
+        store_fp8(key, value, kv_cache, slot_mapping, layout="aos")
+        return
     _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
     _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
     store(key, value, kv_cache, slot_mapping, PiT, midpoints, None, layout="aos",
