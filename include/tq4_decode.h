@@ -152,6 +152,39 @@ int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *
                   uint8_t *kv_cache, int N, int Hk, int D, int block_size, int64_t cache_block_stride,
                   int layout, tq4_stream_t stream);
 
+/*
+ * Bit-width presets: turboquant_k3v4_nc (key_bits 3, value_bits 4), turboquant_3bit_nc
+ * (3, 3) and the 4-bit layout (4, 4), reference/config.py:20-40.  Codes are packed at
+ * key_bits (value_bits) bits per dim, least significant bit first (code d at bits
+ * [b*d, b*d + b) of the row).  SoA record 16*key_bits + 16*value_bits bytes with the three
+ * fp16 metadata fields K norm (folded norm correction), V scale, V zero; AoS slot
+ * K | fp16 norm | V | fp16 scale | fp16 zero padded to even (118 bytes for 3/4, 102 for 3/3).
+ * centroids: the 2^key_bits Lloyd-Max centroids.  Same mid_o contract, grid rule and sinks
+ * as tq4_stage1_ex; runs on the VALU kernel.
+ * Replaces: _tq_decode_stage1 with MSE_BITS = 3 / VQB = 3, reference/soa_decode_v1.py:122-132
+ *           (3-bit K unpack) and :271-284 (3-bit V unpack); the AoS kernel
+ *           reference/aos_decode.py:121-285.
+ */
+int tq4_stage1_preset(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+                      const int32_t *seq_lens, const float *centroids, float *mid_o, int B, int Hq,
+                      int Hk, int D, int block_size, int max_blocks_per_seq,
+                      int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+                      const float *sinks, int key_bits, int value_bits, tq4_stream_t stream);
+
+/*
+ * Writer of the bit-width presets (layout as tq4_stage1_preset): K index = number of the
+ * 2^key_bits - 1 midpoints <= y, V scale = max((max - min) / (2^value_bits - 1), 1e-8);
+ * otherwise as tq4_store (4/4 is tq4_store itself).
+ * Replaces: triton_turboquant_store with MSE bits 3 / value bits 3,
+ *           reference/soa_store.py:300-340 (3-bit K pack) and :47-83 (3-bit V pack); the AoS
+ *           writer reference/aos_store.py.
+ */
+int tq4_store_preset(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
+                     const float *rot_t, const float *midpoints, const float *centroids,
+                     uint8_t *kv_cache, int N, int Hk, int D, int block_size,
+                     int64_t cache_block_stride, int layout, int norm_correction, int key_bits,
+                     int value_bits, tq4_stream_t stream);
+
 /* Message of the last failed call on this thread ("" when none).
  * Replaces: the TORCH_CHECK messages of cuda/tq4_cuda_v1.cu:468-499. */
 const char *tq4_last_error(void);

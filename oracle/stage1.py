@@ -53,6 +53,23 @@ def decode_kv(cache, blocks, offs, kvh, centroids, is_aos, block_size, num_kv_he
     return k, v
 
 
+def decode_kv_bits(cache, blocks, offs, kvh, centroids, is_aos, block_size, num_kv_heads, head_dim,
+                   key_bits, value_bits):
+    """The ``key_bits`` / ``value_bits`` presets (``reference/soa_decode_v1.py:122-132``,
+    ``:271-284``): float64 ``(K, V)``, K = c[idx] * stored norm (AoS: c[idx] renormalised,
+    ``reference/aos_decode.py:197-205``)."""
+    from . import bits
+
+    c = np.asarray(centroids, dtype=np.float64)
+    k_idx, k_norm, v_code, v_scale, v_zero = bits.gather(cache, blocks, offs, kvh, block_size,
+                                                         num_kv_heads, head_dim, key_bits,
+                                                         value_bits, is_aos)
+    cv = c[k_idx]
+    if is_aos:
+        cv = cv / np.sqrt((cv * cv).sum(axis=1, keepdims=True) + 1e-16)
+    return cv * k_norm[:, None], v_code.astype(np.float64) * v_scale[:, None] + v_zero[:, None]
+
+
 def decode_kv_fp8(cache, blocks, offs, kvh, is_aos, block_size, num_kv_heads, head_dim):
     """FP8-key preset: float64 ``(K [T, D], V [T, D])``; K is the E4M3 value of each byte
     (``reference/soa_decode_v1.py:213-230`` with KEY_FP8), no norm."""
@@ -64,12 +81,15 @@ def decode_kv_fp8(cache, blocks, offs, kvh, is_aos, block_size, num_kv_heads, he
 
 
 def stage1(q_rot, cache, block_table, seq_lens, centroids, num_splits, *, num_kv_heads,
-           block_size=16, is_aos=False, attn_scale=None, mid_o=None, sinks=None, key_fp8=False):
+           block_size=16, is_aos=False, attn_scale=None, mid_o=None, sinks=None, key_fp8=False,
+           bits=None):
     """Return ``mid_o`` float64 ``[B, Hq, S, D+1]``; empty splits keep their prior value
     (NaN when ``mid_o`` is not given).  ``sinks`` ``[Hq]``: split 0 of every sequence starts
     its softmax with max = sink and sum = 1, an extra logit with a zero value
     (``reference/soa_decode_v1.py:134-148``).  ``key_fp8``: the FP8-key preset; ``q_rot``
-    is then the unrotated query and ``centroids`` is unused."""
+    is then the unrotated query and ``centroids`` is unused.  ``bits`` ``(key_bits,
+    value_bits)``: the bit-width preset layout of ``oracle.bits`` (``centroids`` has
+    ``2^key_bits`` entries)."""
     q = np.asarray(q_rot, dtype=np.float64)
     batch, num_q_heads, head_dim = q.shape
     group = num_q_heads // num_kv_heads
@@ -90,6 +110,9 @@ def stage1(q_rot, cache, block_table, seq_lens, centroids, num_splits, *, num_kv
                 if key_fp8:
                     k, v = decode_kv_fp8(cache, blocks, offs, kvh, is_aos, block_size,
                                          num_kv_heads, head_dim)
+                elif bits is not None:
+                    k, v = decode_kv_bits(cache, blocks, offs, kvh, centroids, is_aos, block_size,
+                                          num_kv_heads, head_dim, *bits)
                 else:
                     k, v = decode_kv(cache, blocks, offs, kvh, centroids, is_aos,
                                      block_size, num_kv_heads, head_dim)

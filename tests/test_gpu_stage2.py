@@ -140,7 +140,7 @@ def test_backend_decode_entry(dev, layout):
     print(f"{layout} decode entry fp16 max-abs {err:.3e}")
     assert err <= 1e-3
     assert np.abs(lse_buf[:5].cpu().numpy()[live] - rl[live]).max() <= 1e-4
-    with pytest.raises(RuntimeError):  # 3-bit keys are not built
+    with pytest.raises(RuntimeError):  # a 4-bit cache read with 3-bit arguments is rejected
         mod.triton_turboquant_decode_attention(
             t(query), t(cache), t(w.block_table), t(w.seq_lens), t(rot_t.T.copy()), t(w.centroids),
             128 ** -0.5, mse_bits=3, key_packed_size=50, value_quant_bits=4)

@@ -16,10 +16,26 @@
 
 namespace tq4 {
 
+// Code d of a row packed at B bits per code, least significant bit first (code d at bits
+// [B*d, B*d + B) of the byte string, read as little-endian words w); d is a constant after
+// unrolling, so the word index and shifts are too.
+template <int B> __device__ __forceinline__ uint32_t code_at(const uint32_t *w, int d) {
+    const int bit = B * d, wi = bit >> 5, sh = bit & 31;
+    uint32_t v = w[wi] >> sh;
+    if (sh + B > 32)
+        v |= w[wi + 1] << (32 - sh);
+    return v & ((1u << B) - 1u);
+}
+
 // KF8: the FP8-key preset -- K is one E4M3 byte per dim (no codebook, no norm, the query
 // is not rotated); record D + D/2 bytes (SoA; two metadata fields: V scale, V zero) or a
 // D + D/2 + 4 byte slot (AoS: V scale and zero after the V codes).
-template <int LAYOUT, int G, bool KF8 = false>
+// KB > 0: the KB-bit key / VB-bit value presets (turboquant_k3v4_nc, turboquant_3bit_nc,
+// and 4/4), reference/config.py:20-40, with the codes packed at KB (VB) bits per dim
+// (reference/soa_decode_v1.py:122-132, :271-284): record 16 KB + 16 VB bytes (SoA; three
+// metadata fields: K norm, V scale, V zero) or a slot K | norm | V | scale | zero padded to
+// even (AoS); the pair_lut argument then holds the 2^KB centroids themselves.
+template <int LAYOUT, int G, bool KF8 = false, int KB = 0, int VB = 4>
 __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
@@ -39,8 +55,12 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
     __shared__ float pw[G][kWave];
     __shared__ uint32_t vstage[kWave][kHalfD / 4 + 1];  // +1 word: bank spread
 
-    if (!KF8 && lane < 16)
+    if constexpr (KB > 0) {
+        if (lane < (1 << KB))
+            lut[lane] = pair_lut[lane];
+    } else if (!KF8 && lane < 16) {
         lut[lane] = pair_lut[2 * (lane * 16)];  // row (lane, 0) = (c[lane], c[0])
+    }
     for (int i = lane; i < G * kHeadDim; i += kWave) {
         const int h = i / kHeadDim, d = i % kHeadDim;
         qs[h][d] = q_rot[((int64_t)b * num_q_heads + kvh * G + h) * kHeadDim + d];
@@ -67,7 +87,26 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
         const int off = tc % block_size;
         const uint8_t *kp, *vp;
         float norm, vscale, vzero;
-        if constexpr (KF8) {
+        constexpr int kKBytes = 16 * (KB > 0 ? KB : 4), kVBytes = 16 * VB;
+        if constexpr (KB > 0) {
+            if (LAYOUT == 0) {
+                constexpr int rec = kKBytes + kVBytes;
+                kp = cache + blk * block_stride + ((int64_t)off * num_kv_heads + kvh) * rec;
+                vp = kp + kKBytes;
+                const uint8_t *meta = cache + blk * block_stride + (int64_t)block_size * num_kv_heads * rec +
+                                      ((int64_t)kvh * 3 * block_size + off) * 2;
+                norm = load_half(meta);
+                vscale = load_half(meta + 2 * block_size);
+                vzero = load_half(meta + 4 * block_size);
+            } else {
+                constexpr int raw = kKBytes + 2 + kVBytes + 4, slot = raw + raw % 2;
+                kp = cache + blk * block_stride + ((int64_t)off * num_kv_heads + kvh) * slot;
+                norm = load_half(kp + kKBytes);
+                vp = kp + kKBytes + 2;
+                vscale = load_half(vp + kVBytes);
+                vzero = load_half(vp + kVBytes + 2);
+            }
+        } else if constexpr (KF8) {
             constexpr int rec = kHeadDim + kHalfD;
             if (LAYOUT == 0) {
                 kp = cache + blk * block_stride + ((int64_t)off * num_kv_heads + kvh) * rec;
@@ -101,7 +140,24 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
         for (int h = 0; h < G; ++h)
             s[h] = 0.f;
         float csq = 0.f;
-        if constexpr (KF8) {
+        if constexpr (KB > 0) {
+            uint32_t kw[4 * KB];
+#pragma unroll
+            for (int w = 0; w < 4 * KB; ++w)
+                kw[w] = load_u32_a2(kp + 4 * w);
+#pragma unroll
+            for (int d = 0; d < kHeadDim; ++d) {
+                const float c = lut[code_at<KB>(kw, d)];
+                if (LAYOUT == 1)
+                    csq += c * c;
+#pragma unroll
+                for (int h = 0; h < G; ++h)
+                    s[h] += qs[h][d] * c;
+            }
+#pragma unroll
+            for (int w = 0; w < 4 * VB; ++w)
+                vstage[lane][w] = load_u32_a2(vp + 4 * w);
+        } else if constexpr (KF8) {
             for (int w = 0; w < kHeadDim / 4; ++w) {
                 const uint32_t word = load_u32_a2(kp + 4 * w);
                 const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
@@ -150,9 +206,21 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
         __syncthreads();
         const int ntok = min(kWave, r.end - t0);
         for (int j = 0; j < ntok; ++j) {
-            const uint32_t word = vstage[j][lane >> 2];
-            const uint32_t byte = (word >> (8 * (lane & 3))) & 0xFFu;
-            const float c0 = (float)(byte & 15u), c1 = (float)(byte >> 4);
+            float c0, c1;
+            if constexpr (VB == 4) {
+                const uint32_t word = vstage[j][lane >> 2];
+                const uint32_t byte = (word >> (8 * (lane & 3))) & 0xFFu;
+                c0 = (float)(byte & 15u);
+                c1 = (float)(byte >> 4);
+            } else {
+                // dims 2 lane, 2 lane + 1 at bits 2 VB lane .. 2 VB lane + 2 VB - 1 of the
+                // record (a word pair; the second word may be the row's pad word, masked off)
+                const int bit = 2 * VB * lane, wi = bit >> 5;
+                const uint64_t win = (uint64_t)vstage[j][wi] | ((uint64_t)vstage[j][wi + 1] << 32);
+                const uint32_t pair = (uint32_t)(win >> (bit & 31));
+                c0 = (float)(pair & ((1u << VB) - 1u));
+                c1 = (float)((pair >> VB) & ((1u << VB) - 1u));
+            }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 const float pp = pw[h][j];

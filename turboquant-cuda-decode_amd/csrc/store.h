@@ -115,6 +115,25 @@ __device__ __forceinline__ uint16_t half_bits(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// Code j of a lane's 32 dims at B bits per code, least significant bit first (code j at
+// bits [B*j, B*j + B) of the words w); j is a constant after unrolling.
+template <int B, int N> __device__ __forceinline__ void put_code(uint32_t (&w)[N], int j, uint32_t c) {
+    const int bit = B * j, wi = bit >> 5, sh = bit & 31;
+    w[wi] |= c << sh;
+    if (sh + B > 32)
+        w[wi + 1] |= c >> (32 - sh);
+}
+
+// 2-byte stores of N words at a 2-byte aligned address.
+template <int N> __device__ __forceinline__ void store_words_a2(uint8_t *p, const uint32_t (&w)[N]) {
+    uint16_t *h = reinterpret_cast<uint16_t *>(p);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        h[2 * i] = (uint16_t)(w[i] & 0xFFFFu);
+        h[2 * i + 1] = (uint16_t)(w[i] >> 16);
+    }
+}
+
 // 2-byte stores of 16 bytes at a 2-byte aligned address (AoS slots).
 __device__ __forceinline__ void store16_a2(uint8_t *p, uint4 v) {
     uint16_t *h = reinterpret_cast<uint16_t *>(p);
@@ -126,13 +145,15 @@ __device__ __forceinline__ void store16_a2(uint8_t *p, uint4 v) {
     }
 }
 
-// V of one row chunk (the lane's 32 dims; the row's four lanes n + 16g reduce together):
-// scale = max((max - min) / 15, 1e-8), code = clamp(int((v - min) / scale + 0.5), 0, 15),
-// packed two per byte (element j at bits 4(j % 8) of word j / 8).  The product with the
-// reciprocal is within 2^-18 of the fp32 quotient for quotients below 16, so the code only
-// differs when quotient + 0.5 lies within 2^-16 of an integer: those elements take the
-// division.
-__device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[4], float &scale, float &vmin) {
+// V of one row chunk (the lane's 32 dims; the row's four lanes n + 16g reduce together) at
+// VB bits: top = 2^VB - 1, scale = max((max - min) / top, 1e-8), code = clamp(int((v - min) /
+// scale + 0.5), 0, top), packed at VB bits per code (4 bits: element j at bits 4(j % 8) of
+// word j / 8).  The product with the reciprocal is within 2^-18 of the fp32 quotient for
+// quotients below 16, so the code only differs when quotient + 0.5 lies within 2^-16 of an
+// integer: those elements take the division.
+template <int VB = 4>
+__device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[VB], float &scale, float &vmin) {
+    constexpr int kTop = (1 << VB) - 1;
     float lo = x[0], hi = x[0];
 #pragma unroll
     for (int i = 1; i < 32; ++i) {
@@ -141,11 +162,11 @@ __device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[
     }
     vmin = row_min(lo);
     const float vmax = row_max(hi);
-    scale = (vmax - vmin) / 15.0f;
+    scale = (vmax - vmin) / (float)kTop;
     scale = scale > 1e-8f ? scale : 1e-8f;
     const float rs = 1.f / scale;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < VB; ++q)
         vw[q] = 0u;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
@@ -155,11 +176,15 @@ __device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[
             f = (x[j] - vmin) / scale + 0.5f;
         }
         const int c = (int)f;
-        vw[j / 8] |= (uint32_t)(c < 0 ? 0 : (c > 15 ? 15 : c)) << (4 * (j % 8));
+        put_code<VB>(vw, j, (uint32_t)(c < 0 ? 0 : (c > kTop ? kTop : c)));
     }
 }
 
-template <int LAYOUT, class T>
+// KB / VB: bits per K index / V code -- 4 / 4 is the turboquant_4bit_nc layout above;
+// 3 / 4 (turboquant_k3v4_nc) and 3 / 3 (turboquant_3bit_nc) pack 8 codes in 3 bytes
+// (reference/soa_store.py:319-337, :47-83): SoA record 16 KB + 16 VB bytes, AoS slot
+// K | norm | V | scale | zero padded to even, written with 2-byte stores.
+template <int LAYOUT, class T, int KB = 4, int VB = 4>
 __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4))) void store_kernel(
     const T *__restrict__ key, const T *__restrict__ value, const int32_t *__restrict__ slot_mapping,
     const float *__restrict__ pit, const float *__restrict__ midpoints, const float *__restrict__ centroids,
@@ -167,6 +192,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
     int norm_correction) {
     __shared__ __align__(16) _Float16 pt_hi[kHeadDim * kHeadDim];
     __shared__ __align__(16) _Float16 pt_lo[kHeadDim * kHeadDim];
+    constexpr int kMids = (1 << KB) - 1;  // Lloyd-Max midpoints
     __shared__ float c2tab[16];
     __shared__ __align__(16) float4 btab[kCells];
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -201,15 +227,15 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
         *reinterpret_cast<half8 *>(pt_hi + pt_off(c, k8)) = h;
         *reinterpret_cast<half8 *>(pt_lo + pt_off(c, k8)) = l;
     }
-    if (threadIdx.x < 16)
+    if (threadIdx.x <= kMids)
         c2tab[threadIdx.x] = norm_correction ? centroids[threadIdx.x] * centroids[threadIdx.x] : 0.f;
-    float mid[15];
+    float mid[kMids];
 #pragma unroll
-    for (int i = 0; i < 15; ++i)
+    for (int i = 0; i < kMids; ++i)
         mid[i] = midpoints[i];
     float mmin = mid[0], mmax = mid[0];
 #pragma unroll
-    for (int i = 1; i < 15; ++i) {
+    for (int i = 1; i < kMids; ++i) {
         mmin = fminf(mmin, mid[i]);
         mmax = fmaxf(mmax, mid[i]);
     }
@@ -222,7 +248,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
         int base = 0, inside = 0;
         float m_in = __builtin_nanf("");  // compares false with every y
 #pragma unroll
-        for (int i = 0; i < 15; ++i) {
+        for (int i = 0; i < kMids; ++i) {
             base += mid[i] < lo ? 1 : 0;
             if (mid[i] >= lo && mid[i] <= hi) {
                 ++inside;
@@ -230,7 +256,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
             }
         }
         cell_ok = inside <= 1 && w > 0.f && w < __builtin_inff();
-        const int up = base < 15 ? base + 1 : 15;
+        const int up = base < kMids ? base + 1 : kMids;
         // the midpoint is stored x 256, the scale of the rotation's results
         btab[k] = float4{256.f * m_in, __builtin_bit_cast(float, base),
                          norm_correction ? centroids[base] * centroids[base] : 0.f,
@@ -287,8 +313,11 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
             }
         }
         // lane (n, g): acc[j / 4][j % 4] = 256 * y[row n][32g + j]
-        // K indices as nibbles: element j at bits 4(j % 8) of word j / 8
-        uint32_t kw[4] = {0u, 0u, 0u, 0u};
+        // K indices at KB bits (4 bits: element j at bits 4(j % 8) of word j / 8)
+        uint32_t kw[KB];
+#pragma unroll
+        for (int q = 0; q < KB; ++q)
+            kw[q] = 0u;
         float csq = 0.f;
         if (use_cells) {
 #pragma unroll
@@ -299,7 +328,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
                     const float t = fminf(fmaxf(fmaf(a, inv_w, c0), 0.f), (float)(kCells - 1));
                     const float4 e = btab[(int)t];
                     const bool ge = a >= e.x;
-                    kw[q] |= (uint32_t)(__builtin_bit_cast(int, e.y) + (ge ? 1 : 0)) << (4 * (j % 8));
+                    put_code<KB>(kw, j, (uint32_t)(__builtin_bit_cast(int, e.y) + (ge ? 1 : 0)));
                     csq += ge ? e.w : e.z;
                 }
                 // at most 8 table reads in flight (32 VGPRs)
@@ -311,9 +340,9 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
                 const float y = acc[j / 4][j % 4] * (1.f / 256.f);
                 int c = 0;
 #pragma unroll
-                for (int i = 0; i < 15; ++i)
+                for (int i = 0; i < kMids; ++i)
                     c += y >= mid[i] ? 1 : 0;
-                kw[j / 8] |= (uint32_t)c << (4 * (j % 8));
+                put_code<KB>(kw, j, (uint32_t)c);
                 csq += c2tab[c];
             }
         }
@@ -325,14 +354,42 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
             load_raw(vr, value + (int64_t)row * kHeadDim + 32 * g, in_range);
         to_floats(x, vr);
         float scale, vmin;
-        uint32_t vw[4];
-        quantize_v(x, vw, scale, vmin);
-
+        uint32_t vw[VB];
+        quantize_v<VB>(x, vw, scale, vmin);
         const int slot = in_range ? slot_mapping[tok] : -1;
-        if (slot >= 0) {
+        if (KB != 4 || VB != 4) {
+            if (slot >= 0) {
+                const int64_t blk = slot / block_size, off = slot % block_size;
+                uint8_t *base = cache + blk * block_stride;
+                constexpr int kK = 16 * KB, kV = 16 * VB;
+                if constexpr (LAYOUT == 0) {
+                    uint8_t *rec = base + (off * num_kv_heads + head) * (kK + kV);
+                    store_words_a2(rec + 4 * KB * g, kw);
+                    store_words_a2(rec + kK + 4 * VB * g, vw);
+                    if (g == 0) {
+                        uint16_t *meta = reinterpret_cast<uint16_t *>(base + (int64_t)block_size * num_kv_heads * (kK + kV)) +
+                                         (int64_t)head * 3 * block_size + off;
+                        meta[0] = half_bits(kscalar);
+                        meta[block_size] = half_bits(scale);
+                        meta[2 * block_size] = half_bits(vmin);
+                    }
+                } else {
+                    constexpr int raw = kK + 2 + kV + 4, slot_bytes = raw + raw % 2;
+                    uint8_t *sl = base + (off * num_kv_heads + head) * slot_bytes;
+                    store_words_a2(sl + 4 * KB * g, kw);
+                    store_words_a2(sl + kK + 2 + 4 * VB * g, vw);
+                    if (g == 0) {
+                        reinterpret_cast<uint16_t *>(sl + kK)[0] = half_bits(kscalar);
+                        reinterpret_cast<uint16_t *>(sl + kK + 2 + kV)[0] = half_bits(scale);
+                        reinterpret_cast<uint16_t *>(sl + kK + 4 + kV)[0] = half_bits(vmin);
+                    }
+                }
+            }
+        } else if (slot >= 0) {
             const int64_t blk = slot / block_size, off = slot % block_size;
             uint8_t *base = cache + blk * block_stride;
-            const uint4 kb = uint4{kw[0], kw[1], kw[2], kw[3]}, vb = uint4{vw[0], vw[1], vw[2], vw[3]};
+            const uint4 kb = uint4{kw[0], kw[KB > 1 ? 1 : 0], kw[KB > 2 ? 2 : 0], kw[KB > 3 ? 3 : 0]},
+                        vb = uint4{vw[0], vw[VB > 1 ? 1 : 0], vw[VB > 2 ? 2 : 0], vw[VB > 3 ? 3 : 0]};
             if constexpr (LAYOUT == 0) {
                 uint8_t *rec = base + (off * num_kv_heads + head) * kSoaRecord;
                 *reinterpret_cast<uint4 *>(rec + 16 * g) = kb;
@@ -400,7 +457,7 @@ __global__ __launch_bounds__(kWave *kFp8Waves) void store_fp8_kernel(const T *__
         to_floats(x, vr);
         float scale, vmin;
         uint32_t vw[4];
-        quantize_v(x, vw, scale, vmin);
+        quantize_v<4>(x, vw, scale, vmin);
         const int tok = in_range ? row / num_kv_heads : 0;
         const int head = in_range ? row % num_kv_heads : 0;
         const int slot = in_range ? slot_mapping[tok] : -1;

@@ -87,7 +87,20 @@ struct Stage1Args {
     int out_dtype = TQ4_F32;
     float *lse = nullptr;
     bool key_fp8 = false;  // the FP8-key preset (VALU kernel; pair LUT unused)
+    // > 0: the key_bits / value_bits preset on the VALU kernel; lut holds the 2^key_bits
+    // centroids (not the pair LUT)
+    int key_bits = 0, value_bits = 4;
 };
+
+// Bytes of one AoS slot (= SoA bytes per (token, kv-head)) of a key_bits / value_bits preset.
+int preset_slot_bytes(int key_bits, int value_bits) {
+    const int raw = 16 * key_bits + 2 + 16 * value_bits + 4;
+    return raw + raw % 2;
+}
+
+bool preset_supported(int key_bits, int value_bits) {
+    return (key_bits == 4 && value_bits == 4) || (key_bits == 3 && (value_bits == 3 || value_bits == 4));
+}
 static_assert(tq4::kOutF32 == TQ4_F32 && tq4::kOutBf16 == TQ4_BF16 && tq4::kOutF16 == TQ4_F16,
               "output type ids");
 
@@ -103,7 +116,8 @@ int check_stage1(const Stage1Args &a) {
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: head_dim %d unsupported (kernels are built for 128)", a.D);
     if (a.layout != TQ4_LAYOUT_SOA && a.layout != TQ4_LAYOUT_AOS)
         return fail(TQ4_E_INVALID, "tq4_stage1: layout must be 0 (SoA) or 1 (AoS)");
-    const int slot = a.key_fp8 ? tq4::store::kFp8Record + 4 : tq4::kAosSlot;
+    const int slot = a.key_fp8 ? tq4::store::kFp8Record + 4
+                               : (a.key_bits > 0 ? preset_slot_bytes(a.key_bits, a.value_bits) : tq4::kAosSlot);
     const int64_t min_stride = (int64_t)a.bs * a.Hk * slot;
     if (a.stride < min_stride || a.stride % 2)
         return fail(TQ4_E_INVALID, "tq4_stage1: requires cache [blocks,%d,%d,%d]: block stride %lld < %lld",
@@ -117,8 +131,15 @@ int check_stage1(const Stage1Args &a) {
 
 template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t st) {
     const dim3 grid(a.S, a.Hk, a.B);
-    const auto kernel = a.key_fp8 ? &tq4::stage1_simple_kernel<LAYOUT, G, true>
-                                  : &tq4::stage1_simple_kernel<LAYOUT, G, false>;
+    auto kernel = &tq4::stage1_simple_kernel<LAYOUT, G, false>;
+    if (a.key_fp8)
+        kernel = &tq4::stage1_simple_kernel<LAYOUT, G, true>;
+    else if (a.key_bits == 4)
+        kernel = &tq4::stage1_simple_kernel<LAYOUT, G, false, 4, 4>;
+    else if (a.key_bits == 3 && a.value_bits == 4)
+        kernel = &tq4::stage1_simple_kernel<LAYOUT, G, false, 3, 4>;
+    else if (a.key_bits == 3)
+        kernel = &tq4::stage1_simple_kernel<LAYOUT, G, false, 3, 3>;
     launch(kernel, grid, dim3(tq4::kWave), st,
                        a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.sinks, a.Hq, a.Hk, a.bs,
                        a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
@@ -258,8 +279,10 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     // The FP8-key preset runs on the VALU kernel.
     if (a.key_fp8 && kernel != TQ4_KERNEL_AUTO && kernel != TQ4_KERNEL_SIMPLE)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: FP8 keys run on the VALU kernel");
+    if (a.key_bits > 0 && kernel != TQ4_KERNEL_AUTO && kernel != TQ4_KERNEL_SIMPLE)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_preset: the bit-width presets run on the VALU kernel");
     if (kernel == TQ4_KERNEL_AUTO)
-        kernel = a.key_fp8 ? TQ4_KERNEL_SIMPLE : (mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE);
+        kernel = a.key_fp8 || a.key_bits > 0 ? TQ4_KERNEL_SIMPLE : (mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE);
     if (kernel == TQ4_KERNEL_MFMA && a.sinks)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_ex: sinks need the XDL or the VALU kernel");
     if (kernel == TQ4_KERNEL_MFMA)
@@ -301,6 +324,32 @@ int rotate_query(const void *query, int query_dtype, const float *rot_t, float *
     return launch_status("rotate_query");
 }
 
+// The writer for KB-bit K indices / VB-bit V codes over `rows` (token, kv-head) rows.
+template <int KB, int VB>
+int launch_store(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
+                 const float *rot_t, const float *midpoints, const float *centroids, uint8_t *kv_cache,
+                 int rows, int Hk, int block_size, int64_t cache_block_stride, int layout,
+                 int norm_correction, hipStream_t st, const char *what) {
+    const int per_group = tq4::store::kRows * tq4::store::kWaves;
+    const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, tq4::store::kMaxGroups));
+#define TQ4_STORE_LAUNCH(L, T)                                                                            \
+    launch(&tq4::store::store_kernel<L, T, KB, VB>, grid, dim3(tq4::kWave * tq4::store::kWaves), st,      \
+           static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, midpoints,      \
+           centroids, kv_cache, rows, Hk, block_size, cache_block_stride, norm_correction)
+    switch (dtype * 2 + layout) {
+    case TQ4_F32 * 2 + 0: TQ4_STORE_LAUNCH(0, float); break;
+    case TQ4_F32 * 2 + 1: TQ4_STORE_LAUNCH(1, float); break;
+    case TQ4_BF16 * 2 + 0: TQ4_STORE_LAUNCH(0, __bf16); break;
+    case TQ4_BF16 * 2 + 1: TQ4_STORE_LAUNCH(1, __bf16); break;
+    case TQ4_F16 * 2 + 0: TQ4_STORE_LAUNCH(0, _Float16); break;
+    case TQ4_F16 * 2 + 1: TQ4_STORE_LAUNCH(1, _Float16); break;
+    default:
+        return fail(TQ4_E_INVALID, "%s: dtype must be 0 (f32), 1 (bf16) or 2 (f16)", what);
+    }
+#undef TQ4_STORE_LAUNCH
+    return launch_status(what);
+}
+
 }  // namespace
 
 extern "C" {
@@ -311,7 +360,7 @@ int tq4_time_next_launch(void *start_event, void *stop_event) {
     return ok();
 }
 
-int tq4_abi_version(void) { return 101; }
+int tq4_abi_version(void) { return 102; }
 
 const char *tq4_last_error(void) { return g_err; }
 
@@ -344,6 +393,22 @@ int tq4_stage1_fp8(const float *query, const uint8_t *kv_cache, const int32_t *b
                  block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
                  attn_scale, sinks};
     a.key_fp8 = true;
+    return run_stage1(a, TQ4_KERNEL_SIMPLE, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tq4_stage1_preset(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+                      const int32_t *seq_lens, const float *centroids, float *mid_o, int B, int Hq,
+                      int Hk, int D, int block_size, int max_blocks_per_seq,
+                      int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+                      const float *sinks, int key_bits, int value_bits, tq4_stream_t stream) {
+    if (!preset_supported(key_bits, value_bits))
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_preset: key_bits / value_bits %d / %d unsupported "
+                                       "(4/4, 3/4, 3/3)", key_bits, value_bits);
+    Stage1Args a{q_rot, kv_cache, block_table, seq_lens, centroids, mid_o, B, Hq, Hk, D,
+                 block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
+                 attn_scale, sinks};
+    a.key_bits = key_bits;
+    a.value_bits = value_bits;
     return run_stage1(a, TQ4_KERNEL_SIMPLE, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -459,26 +524,52 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
                     (long long)N * Hk);
     if (N == 0)
         return ok();
-    const int rows = N * Hk;
-    const int per_group = tq4::store::kRows * tq4::store::kWaves;
-    const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, tq4::store::kMaxGroups));
+    return launch_store<4, 4>(key, value, dtype, slot_mapping, rot_t, midpoints, centroids, kv_cache,
+                              N * Hk, Hk, block_size, cache_block_stride, layout, norm_correction,
+                              reinterpret_cast<hipStream_t>(stream), "tq4_store");
+}
+
+int tq4_store_preset(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
+                     const float *rot_t, const float *midpoints, const float *centroids,
+                     uint8_t *kv_cache, int N, int Hk, int D, int block_size,
+                     int64_t cache_block_stride, int layout, int norm_correction, int key_bits,
+                     int value_bits, tq4_stream_t stream) {
+    if (!preset_supported(key_bits, value_bits))
+        return fail(TQ4_E_UNSUPPORTED, "tq4_store_preset: key_bits / value_bits %d / %d unsupported "
+                                       "(4/4, 3/4, 3/3)", key_bits, value_bits);
+    if (key_bits == 4)
+        return tq4_store(key, value, dtype, slot_mapping, rot_t, midpoints, centroids, kv_cache, N, Hk, D,
+                         block_size, cache_block_stride, layout, norm_correction, stream);
+    if (!key || !value || !slot_mapping || !rot_t || !midpoints || !kv_cache)
+        return fail(TQ4_E_INVALID, "tq4_store_preset: null pointer argument");
+    if (norm_correction && !centroids)
+        return fail(TQ4_E_INVALID, "tq4_store_preset: norm_correction requires centroids");
+    if (N < 0 || Hk <= 0 || block_size <= 0)
+        return fail(TQ4_E_INVALID, "tq4_store_preset: N must be >= 0, Hk and block_size positive");
+    if (D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_store_preset: head_dim %d unsupported (128)", D);
+    if (layout != TQ4_LAYOUT_SOA && layout != TQ4_LAYOUT_AOS)
+        return fail(TQ4_E_INVALID, "tq4_store_preset: layout must be 0 (SoA) or 1 (AoS)");
+    const int slot = preset_slot_bytes(key_bits, value_bits);
+    const int64_t min_stride = (int64_t)block_size * Hk * slot;
+    if (cache_block_stride < min_stride || cache_block_stride % 2)
+        return fail(TQ4_E_INVALID, "tq4_store_preset: requires cache [blocks,%d,%d,%d]: block stride %lld",
+                    block_size, Hk, slot, (long long)cache_block_stride);
+    if (!aligned(key, 16) || !aligned(value, 16) || !aligned(kv_cache, 2))
+        return fail(TQ4_E_INVALID, "tq4_store_preset: key and value must be 16-byte aligned, kv_cache 2-byte");
+    if ((int64_t)N * Hk > INT32_MAX - 64)
+        return fail(TQ4_E_INVALID, "tq4_store_preset: N * Hk = %lld rows exceeds the 32-bit row index",
+                    (long long)N * Hk);
+    if (N == 0)
+        return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define TQ4_STORE_LAUNCH(L, T)                                                                       \
-    launch(&tq4::store::store_kernel<L, T>, grid, dim3(tq4::kWave * tq4::store::kWaves), st,         \
-           static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, midpoints, \
-           centroids, kv_cache, rows, Hk, block_size, cache_block_stride, norm_correction)
-    switch (dtype * 2 + layout) {
-    case TQ4_F32 * 2 + 0: TQ4_STORE_LAUNCH(0, float); break;
-    case TQ4_F32 * 2 + 1: TQ4_STORE_LAUNCH(1, float); break;
-    case TQ4_BF16 * 2 + 0: TQ4_STORE_LAUNCH(0, __bf16); break;
-    case TQ4_BF16 * 2 + 1: TQ4_STORE_LAUNCH(1, __bf16); break;
-    case TQ4_F16 * 2 + 0: TQ4_STORE_LAUNCH(0, _Float16); break;
-    case TQ4_F16 * 2 + 1: TQ4_STORE_LAUNCH(1, _Float16); break;
-    default:
-        return fail(TQ4_E_INVALID, "tq4_store: dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
-    }
-#undef TQ4_STORE_LAUNCH
-    return launch_status("store");
+    if (value_bits == 4)
+        return launch_store<3, 4>(key, value, dtype, slot_mapping, rot_t, midpoints, centroids, kv_cache,
+                                  N * Hk, Hk, block_size, cache_block_stride, layout, norm_correction, st,
+                                  "tq4_store_preset");
+    return launch_store<3, 3>(key, value, dtype, slot_mapping, rot_t, midpoints, centroids, kv_cache,
+                              N * Hk, Hk, block_size, cache_block_stride, layout, norm_correction, st,
+                              "tq4_store_preset");
 }
 
 int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *slot_mapping,

@@ -11,7 +11,7 @@ __all__ = [
     "rotate_query", "pair_lut_device", "launch_tq4_v2_stage1", "launch_soa_v1_stage1",
     "launch_aos_v1_stage1", "launch_stage2", "ext", "DecodeWorkspace", "Tq4Error", "store",
     "triton_turboquant_store", "aos_triton_turboquant_store", "turboquant_decode_attention",
-    "stage1_fp8", "store_fp8",
+    "stage1_fp8", "store_fp8", "stage1_preset", "store_preset",
 ]
 
 

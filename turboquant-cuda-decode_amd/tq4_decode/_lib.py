@@ -26,6 +26,8 @@ EXPORTS = (
     "tq4_store",
     "tq4_stage1_fp8",
     "tq4_store_fp8",
+    "tq4_stage1_preset",
+    "tq4_store_preset",
     "tq4_last_error",
     "tq4_abi_version",
     "tq4_time_next_launch",
@@ -48,6 +50,9 @@ _SIGS = {
     "tq4_time_next_launch": [_p, _p],
     "tq4_stage1_fp8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _p],
     "tq4_store_fp8": [_p, _p, _i, _p, _p, _i, _i, _i, _i, _i64, _i, _p],
+    "tq4_stage1_preset": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _i,
+                          _i, _p],
+    "tq4_store_preset": [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _i, _i, _p],
 }
 
 

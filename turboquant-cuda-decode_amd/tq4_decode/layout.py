@@ -31,6 +31,14 @@ def slot_bytes(head_dim: int) -> int:
     return raw + raw % 2
 
 
+def slot_bytes_preset(head_dim: int, key_bits: int, value_bits: int) -> int:
+    """Slot of the ``key_bits`` / ``value_bits`` presets (``reference/config.py:128-164``):
+    K codes + fp16 norm + V codes + fp16 scale + fp16 zero, rounded up to even (3/4: 118,
+    3/3: 102, 4/4: 134 at D = 128)."""
+    raw = head_dim * key_bits // 8 + 2 + head_dim * value_bits // 8 + 4
+    return raw + raw % 2
+
+
 def slot_bytes_fp8(head_dim: int) -> int:
     """FP8-key preset slot: one E4M3 byte per K dim + V codes + fp16 V scale and zero
     (``reference/config.py:128-164``)."""

@@ -14,7 +14,7 @@ Reference call shapes kept here:
 * ``launch_stage2(mid_o, seq_lens, output, lse)`` -- ``baseline/stage2.py:58-81``
 * ``triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits,
   key_packed_size, value_quant_bits, key_fp8=False, centroids=None, norm_correction=False)``
-  -- ``reference/soa_store.py:381-524`` (4-bit keys and values)
+  -- ``reference/soa_store.py:381-524`` (4-bit, 3-bit-key and 3-bit presets, FP8 keys)
 * ``ext`` -- object with the CUDA-extension names ``tq4_cuda_v1 .. tq4_cuda_v9``,
   ``tq4_cuda_v7_stage1 / _stage2 / _full`` (``cuda/tq4_cuda_v7_bind.cpp:3-20``), so
   ``cuda_ext = tq4_decode.ext`` drops into ``benchmarks/stage1.py`` / ``full_decode.py``.
@@ -27,7 +27,7 @@ import torch
 
 from . import _lib
 from ._lib import Tq4Error  # noqa: F401  (raised by every wrapper)
-from .layout import AOS, LAYOUTS, SOA, slot_bytes, slot_bytes_fp8
+from .layout import AOS, LAYOUTS, SOA, slot_bytes, slot_bytes_fp8, slot_bytes_preset
 
 KERNELS = {"auto": 0, "simple": 1, "mfma": 2, "xdl": 3}
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -255,6 +255,86 @@ def store_fp8(key, value, kv_cache, slot_mapping, *, layout="soa"):
     return kv_cache
 
 
+PRESETS = ((4, 4), (3, 4), (3, 3))  # (key bits, value bits) of the MSE-key presets
+
+
+def stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o=None, *, key_bits,
+                  value_bits, num_kv_splits=None, layout="soa", attn_scale=None, sinks=None):
+    """Stage1 of the bit-width presets (``turboquant_k3v4_nc``: 3/4, ``turboquant_3bit_nc``:
+    3/3, and 4/4) on the VALU kernel: ``q_rot`` fp32 ``[B, Hq, D]``, ``centroids`` the
+    ``2^key_bits`` Lloyd-Max centroids; returns ``mid_o [B, Hq, S, D+1]``."""
+    _require((key_bits, value_bits) in PRESETS, f"key/value bits must be one of {PRESETS}")
+    for t, n, dt in ((q_rot, "q_rot", torch.float32), (kv_cache, "kv_cache", torch.uint8),
+                     (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
+                     (centroids, "centroids", torch.float32)):
+        _check_tensor(t, n, dt)
+    _require(q_rot.dim() == 3 and q_rot.size(2) == HEAD_DIM, f"q_rot must be [B, Hq, {HEAD_DIM}]")
+    B, Hq, D = q_rot.shape
+    _require(centroids.numel() == 1 << key_bits, f"{key_bits}-bit keys need {1 << key_bits} centroids")
+    _require(kv_cache.dim() == 4, "kv_cache must be [blocks, block_size, Hk, slot]")
+    _, bs, Hk, slot = kv_cache.shape
+    want = slot_bytes_preset(D, key_bits, value_bits)
+    _require(slot == want, f"requires slot_size={want}")
+    _require(Hq % Hk == 0, "Hq must be a multiple of Hk")
+    _require(block_table.dim() == 2 and block_table.size(0) == B, "block_table batch mismatch")
+    _require(seq_lens.dim() == 1 and seq_lens.size(0) == B, "seq_lens batch mismatch")
+    if mid_o is None:
+        _require(num_kv_splits is not None and num_kv_splits > 0,
+                 "num_kv_splits is required when mid_o is None")
+        mid_o = torch.empty(B, Hq, num_kv_splits, D + 1, dtype=torch.float32, device=q_rot.device)
+    _check_tensor(mid_o, "mid_o", torch.float32)
+    S = mid_o.size(2)
+    _require(tuple(mid_o.shape) == (B, Hq, S, D + 1), f"mid_o must be [B,{Hq},S,{D + 1}]")
+    devs = {t.device for t in (q_rot, kv_cache, block_table, seq_lens, centroids, mid_o)}
+    _require(len(devs) == 1, "all tensors must be on the same device")
+    scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
+    rc = _lib.load().tq4_stage1_preset(
+        q_rot.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
+        centroids.data_ptr(), mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1),
+        kv_cache.stride(0), S, _layout_id(layout), scale, _check_sinks(sinks, Hq, q_rot.device),
+        key_bits, value_bits, _stream(q_rot.device))
+    _lib.check(rc, "tq4_stage1_preset")
+    return mid_o
+
+
+def store_preset(key, value, kv_cache, slot_mapping, rotation_t, midpoints, centroids=None, *,
+                 key_bits, value_bits, layout="soa", norm_correction=True):
+    """Writer of the bit-width presets: K index = number of the ``2^key_bits - 1``
+    ``midpoints`` <= y, V codes at ``value_bits``; otherwise as ``store``."""
+    _require((key_bits, value_bits) in PRESETS, f"key/value bits must be one of {PRESETS}")
+    _require(key.is_cuda and key.dtype in DTYPES and key.is_contiguous(), "invalid key")
+    _require(value.dtype == key.dtype and value.is_contiguous() and value.shape == key.shape,
+             "value must match key (shape, dtype, contiguous)")
+    _require(key.dim() == 3 and key.size(2) == HEAD_DIM, f"key must be [N, Hk, {HEAD_DIM}]")
+    _check_tensor(kv_cache, "kv_cache", torch.uint8)
+    _check_tensor(slot_mapping, "slot_mapping", torch.int32)
+    _check_tensor(rotation_t, "rotation_t", torch.float32)
+    _check_tensor(midpoints, "midpoints", torch.float32)
+    n_mid = (1 << key_bits) - 1
+    _require(midpoints.numel() == n_mid, f"{key_bits}-bit keys need {n_mid} midpoints")
+    _require(tuple(rotation_t.shape) == (HEAD_DIM, HEAD_DIM), f"rotation must be [{HEAD_DIM}, {HEAD_DIM}]")
+    if norm_correction:
+        _require(centroids is not None, "norm_correction=True requires centroids")
+    if centroids is not None:
+        _check_tensor(centroids, "centroids", torch.float32)
+        _require(centroids.numel() == n_mid + 1, f"{key_bits}-bit keys need {n_mid + 1} centroids")
+    N, Hk, D = key.shape
+    want = slot_bytes_preset(D, key_bits, value_bits)
+    _require(kv_cache.dim() == 4 and kv_cache.size(2) == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
+    _require(kv_cache.size(3) == want, f"requires slot_size={want}")
+    _require(slot_mapping.numel() == N, "slot_mapping must have one entry per token")
+    devs = {t.device for t in (key, value, kv_cache, slot_mapping, rotation_t, midpoints)}
+    _require(len(devs) == 1, "all tensors must be on the same device")
+    rc = _lib.load().tq4_store_preset(
+        key.data_ptr(), value.data_ptr(), DTYPES[key.dtype], slot_mapping.data_ptr(),
+        rotation_t.data_ptr(), midpoints.data_ptr(),
+        centroids.data_ptr() if centroids is not None else None, kv_cache.data_ptr(), N, Hk, D,
+        kv_cache.size(1), kv_cache.stride(0), _layout_id(layout), int(bool(norm_correction)),
+        key_bits, value_bits, _stream(key.device))
+    _lib.check(rc, "tq4_store_preset")
+    return kv_cache
+
+
 class DecodeWorkspace:
     """Preallocated buffers of one full decode step (fixed shapes, reusable)."""
 
@@ -322,16 +402,23 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
     Caller buffers are used when they fit (``mid_o_buf`` fp32 ``[>=B, Hq, S, D+1]``,
     ``output_buf`` ``[>=B, Hq, D]`` in the query dtype, ``lse_buf`` fp32 ``[>=B, Hq]``); the
     rotated query and the pair LUT live on ``buf_holder`` when one is given; ``sinks``
-    (fp32 ``[Hq]``) enter split 0.  Built for the 4-bit ``turboquant_4bit_nc`` cache and,
-    with ``key_fp8``, the ``turboquant_k8v4`` cache (unrotated query, VALU Stage1); other
-    bit widths and 4-bit AoS without norm correction raise ``NotImplementedError``.
+    (fp32 ``[Hq]``) enter split 0.  Built for the 4-bit ``turboquant_4bit_nc`` cache, with
+    ``key_fp8`` the ``turboquant_k8v4`` cache (unrotated query, VALU Stage1), and the 3-bit
+    presets ``turboquant_k3v4_nc`` / ``turboquant_3bit_nc`` (VALU Stage1); 4-bit AoS without
+    norm correction raises ``NotImplementedError``.
     """
-    _require(value_quant_bits == 4, "only 4-bit values are built")
     if key_fp8:
+        _require(value_quant_bits == 4, "FP8 keys are built with 4-bit values")
         return _decode_attention_fp8(query, kv_cache, block_table, seq_lens, scale, key_packed_size,
                                      mid_o_buf, output_buf, lse_buf, buf_holder, max_num_kv_splits,
                                      sinks, layout)
-    _require(mse_bits == 4, "only 4-bit MSE keys are built")
+    _require((mse_bits, value_quant_bits) in PRESETS,
+             f"MSE key / value bits must be one of {PRESETS}")
+    if mse_bits != 4 or value_quant_bits != 4:
+        return _decode_attention_preset(query, kv_cache, block_table, seq_lens, Pi, PiT, centroids,
+                                        scale, mse_bits, key_packed_size, value_quant_bits,
+                                        norm_correction, mid_o_buf, output_buf, lse_buf, buf_holder,
+                                        max_num_kv_splits, sinks, layout)
     _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
     if layout == "aos" and not norm_correction:
         raise NotImplementedError("AoS decode is built with the norm correction (turboquant_4bit_nc)")
@@ -366,6 +453,39 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
     out, _ = full_decode(query.contiguous(), PiT, kv_cache, block_table, seq_lens, centroids, S,
                          layout=layout, out_dtype=query.dtype, attn_scale=scale, workspace=ws,
                          sinks=sinks)
+    return out
+
+
+def _decode_attention_preset(query, kv_cache, block_table, seq_lens, Pi, PiT, centroids, scale,
+                             mse_bits, key_packed_size, value_quant_bits, norm_correction,
+                             mid_o_buf, output_buf, lse_buf, buf_holder, max_num_kv_splits, sinks,
+                             layout):
+    """3-bit-key presets: ``q_rot = query @ PiT`` on the matrix cores, VALU Stage1, Stage2."""
+    if layout == "aos" and not norm_correction:
+        raise NotImplementedError("AoS decode is built with the norm correction (the _nc presets)")
+    want = HEAD_DIM * mse_bits // 8 + 2
+    _require(key_packed_size == want, f"key_packed_size must be {want}")
+    _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
+    B, Hq, D = query.shape
+    S = int(max_num_kv_splits)
+    if PiT is None:
+        PiT = Pi.t().contiguous()
+    q_rot = rotate_query(query.contiguous(), PiT)
+    mid_o = _buffer_view(mid_o_buf, (B, Hq, S, D + 1), torch.float32)
+    if mid_o is None:
+        mid_o = torch.empty(B, Hq, S, D + 1, dtype=torch.float32, device=query.device)
+        if buf_holder is not None:
+            buf_holder._tq_mid_o_buf = mid_o
+    out = _buffer_view(output_buf, (B, Hq, D), query.dtype)
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=query.dtype, device=query.device)
+    lse = _buffer_view(lse_buf, (B, Hq), torch.float32)
+    if lse is None:
+        lse = torch.empty(B, Hq, dtype=torch.float32, device=query.device)
+    stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids.float().contiguous(), mid_o,
+                  key_bits=mse_bits, value_bits=value_quant_bits, layout=layout, attn_scale=scale,
+                  sinks=sinks)
+    stage2(mid_o, seq_lens, out, lse, out_dtype=query.dtype)
     return out
 
 
@@ -424,32 +544,43 @@ def launch_stage2(mid_o, seq_lens, output, lse):
 def triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits,
                             key_packed_size, value_quant_bits, key_fp8=False, centroids=None,
                             norm_correction=False):
-    """SoA cache writer with the ``reference/soa_store.py:381-397`` signature (MSE path,
-    4-bit keys and values; the FP8-key path and other bit widths are not built)."""
+    """SoA cache writer with the ``reference/soa_store.py:381-397`` signature: the MSE-key
+    presets (4/4, 3/4, 3/3 key / value bits) and FP8 keys with 4-bit values."""
     if key_fp8:  # turboquant_k8v4: no rotation, no codebook
         _require(value_quant_bits == 4 and key_packed_size == HEAD_DIM, "FP8 keys need 4-bit values "
                  f"and key_packed_size {HEAD_DIM}")
         store_fp8(key, value, kv_cache, slot_mapping, layout="soa")
         return
-    _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
-    _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
-    store(key, value, kv_cache, slot_mapping, PiT, midpoints, centroids, layout="soa",
-          norm_correction=norm_correction)
+    _store_mse(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits, key_packed_size,
+               value_quant_bits, centroids, norm_correction, "soa")
+
+
+def _store_mse(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits, key_packed_size,
+               value_quant_bits, centroids, norm_correction, layout):
+    _require((mse_bits, value_quant_bits) in PRESETS,
+             f"MSE key / value bits must be one of {PRESETS}")
+    want = HEAD_DIM * mse_bits // 8 + 2
+    _require(key_packed_size == want, f"key_packed_size must be {want}")
+    if mse_bits == 4 and value_quant_bits == 4:
+        store(key, value, kv_cache, slot_mapping, PiT, midpoints, centroids, layout=layout,
+              norm_correction=norm_correction)
+    else:
+        store_preset(key, value, kv_cache, slot_mapping, PiT, midpoints, centroids,
+                     key_bits=mse_bits, value_bits=value_quant_bits, layout=layout,
+                     norm_correction=norm_correction)
 
 
 def aos_triton_turboquant_store(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits,
                                 key_packed_size, value_quant_bits, key_fp8=False):
-    """AoS cache writer with the ``reference/aos_store.py:350-361`` signature (MSE path,
-    4-bit keys and values; the slot keeps the raw fp16 norm, no norm correction)."""
+    """AoS cache writer with the ``reference/aos_store.py:350-361`` signature: the MSE-key
+    presets (the slot keeps the raw fp16 norm, no norm correction) and FP8 keys."""
     if key_fp8:  # turboquant_k8v4: no rotation, no codebook
         _require(value_quant_bits == 4 and key_packed_size == HEAD_DIM, "FP8 keys need 4-bit values "
                  f"and key_packed_size {HEAD_DIM}")
         store_fp8(key, value, kv_cache, slot_mapping, layout="aos")
         return
-    _require(mse_bits == 4 and value_quant_bits == 4, "only 4-bit keys and values are built")
-    _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
-    store(key, value, kv_cache, slot_mapping, PiT, midpoints, None, layout="aos",
-          norm_correction=False)
+    _store_mse(key, value, kv_cache, slot_mapping, PiT, midpoints, mse_bits, key_packed_size,
+               value_quant_bits, None, False, "aos")
 
 
 class _CudaExtCompat:
