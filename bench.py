@@ -196,36 +196,55 @@ def full_decode_time(dev, flush, timer, reps=30):
             "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes}
 
 
-def stage1_fp8_time(dev, flush, timer, reps=30):
-    """Stage1 of the FP8-key preset at the B64 x ctx 4096 shape (32/8 heads, 32 splits),
-    SoA, cold, kernel duration.  Synthetic cache: random E4M3 K bytes (no NaN codes),
-    random 4-bit V codes, fp16 scale/zero in the ranges of the 4-bit workload.  Bytes:
-    196 per token and kv-head + query + block table + mid_o rows."""
+# preset Stage1 workloads: name -> (preset, SoA record bytes, metadata fields)
+PRESET_WORKLOADS = {
+    "stage1_fp8_b64_ctx4096": ("fp8", 192, 2),
+    "stage1_k3v4_b64_ctx4096": ((3, 4), 112, 3),
+    "stage1_3bit_b64_ctx4096": ((3, 3), 96, 3),
+}
+
+
+def stage1_preset_time(dev, flush, timer, name, reps=30):
+    """Stage1 of a preset (FP8 keys: ``tq4_stage1_fp8``; 3-bit keys: ``tq4_stage1_preset``)
+    at the B64 x ctx 4096 shape (32/8 heads, 32 splits), SoA, cold, kernel duration.
+    Synthetic cache: random code bytes (E4M3 without NaN codes for FP8 keys), fp16 K norm /
+    V scale / V zero in the ranges of the 4-bit workload.  Bytes: one slot per token and
+    kv-head + query + block table + mid_o rows."""
     import numpy as np
     import torch
 
-    from tq4_decode import ops, workloads
+    from tq4_decode import codebook, ops, workloads
 
+    preset, rec, fields = PRESET_WORKLOADS[name]
     w = workloads.qwen3_4b_b64_ctx4096()
     rng = np.random.default_rng(11)
     nb, bs, hk = w.kv_cache.shape[0], w.block_size, w.num_kv_heads
-    slot = 196
+    slot = rec + 2 * fields
     cache = rng.integers(0, 256, (nb, bs * hk * slot), dtype=np.uint8)
-    k_region = cache[:, :bs * hk * 192].reshape(nb, bs * hk, 192)[:, :, :128]
-    k_region[(k_region & 0x7F) == 0x7F] = 0x38  # no NaN codes
-    meta = cache[:, bs * hk * 192:].view(np.float16).reshape(nb, hk, 2, bs)
-    meta[:, :, 0] = rng.uniform(0.01, 0.1, (nb, hk, bs)).astype(np.float16)
-    meta[:, :, 1] = rng.uniform(-0.5, 0.5, (nb, hk, bs)).astype(np.float16)
+    if preset == "fp8":
+        k_region = cache[:, :bs * hk * rec].reshape(nb, bs * hk, rec)[:, :, :128]
+        k_region[(k_region & 0x7F) == 0x7F] = 0x38  # no NaN codes
+    meta = cache[:, bs * hk * rec:].view(np.float16).reshape(nb, hk, fields, bs)
+    if fields == 3:
+        meta[:, :, 0] = rng.uniform(0.5, 2.0, (nb, hk, bs)).astype(np.float16)
+    meta[:, :, fields - 2] = rng.uniform(0.01, 0.1, (nb, hk, bs)).astype(np.float16)
+    meta[:, :, fields - 1] = rng.uniform(-0.5, 0.5, (nb, hk, bs)).astype(np.float16)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     q, c = t(w.q_rot), t(cache.reshape(nb, bs, hk, slot))
     bt, sl = t(w.block_table), t(w.seq_lens)
     mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
+    if preset == "fp8":
+        run = lambda: ops.stage1_fp8(q, c, bt, sl, mid)  # noqa: E731
+    else:
+        cents = t(codebook.centroids(w.head_dim, preset[0]).astype(np.float32))
+        run = lambda: ops.stage1_preset(q, c, bt, sl, cents, mid, key_bits=preset[0],  # noqa: E731
+                                        value_bits=preset[1])
     times = []
     for i in range(reps + 3):
         flush.sum()
         a, b = timer.pair()
         timer.stamp_next_launch(a, b)
-        ops.stage1_fp8(q, c, bt, sl, mid)
+        run()
         torch.cuda.synchronize()
         if i >= 3:
             times.append(timer.elapsed_ms(a, b) * 1e3)
@@ -286,12 +305,15 @@ def side_workload(args, dev) -> int:
 
     flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
     timer = HipEvents(torch.cuda.current_stream(dev).cuda_stream)
-    if args.workload == "stage1_fp8_b64_ctx4096":
-        r = stage1_fp8_time(dev, flush, timer, reps=args.steps)
+    if args.workload in PRESET_WORKLOADS:
+        r = stage1_preset_time(dev, flush, timer, args.workload, reps=args.steps)
         us, gbs = r["us"], r["GBps"]
-        metric = "Stage1, FP8-key preset (turboquant_k8v4), B64 x ctx4096 Qwen3-4B shape: GB/s"
+        preset = PRESET_WORKLOADS[args.workload][0]
+        label = {"fp8": "FP8-key preset (turboquant_k8v4)", (3, 4): "3-bit-key preset (turboquant_k3v4_nc)",
+                 (3, 3): "3-bit preset (turboquant_3bit_nc)"}[preset]
+        metric = f"Stage1, {label}, B64 x ctx4096 Qwen3-4B shape: GB/s"
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
-        dtype = "e4m3 K, 4-bit V, f32 math"
+        dtype = ("e4m3 K, 4-bit V" if preset == "fp8" else f"{preset[0]}-bit K, {preset[1]}-bit V") + ", f32 math"
     elif args.workload.startswith("store_"):
         size = args.workload[len("store_"):]
         r = store_times(dev, flush, timer, reps=args.steps, only=size)
@@ -327,7 +349,7 @@ def main() -> int:
                     help="also run a 256 MiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--workload", default="stage1",
                     choices=["stage1", "store_decode_b64", "store_prefill_n8192", "full_decode_b256",
-                             "stage1_fp8_b64_ctx4096"],
+                             *PRESET_WORKLOADS],
                     help="stage1: the headline (default); the others time only that workload "
                          "(--steps cold launches) and print its own JSON line, e.g. for a profile")
     args = ap.parse_args()

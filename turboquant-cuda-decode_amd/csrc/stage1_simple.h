@@ -27,6 +27,26 @@ template <int B> __device__ __forceinline__ uint32_t code_at(const uint32_t *w, 
     return v & ((1u << B) - 1u);
 }
 
+// N little-endian words at p: 16-byte loads when p is 16-byte aligned (SoA records with a
+// 16-byte block stride), else 2-byte loads (AoS slots are only 2-byte aligned).
+template <int N> __device__ __forceinline__ void load_words(uint32_t (&w)[N], const uint8_t *p, bool a16) {
+    static_assert(N % 4 == 0, "whole 16-byte chunks");
+    if (a16) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const uint4 v = reinterpret_cast<const uint4 *>(p)[i];
+            w[4 * i] = v.x;
+            w[4 * i + 1] = v.y;
+            w[4 * i + 2] = v.z;
+            w[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            w[i] = load_u32_a2(p + 4 * i);
+    }
+}
+
 // KF8: the FP8-key preset -- K is one E4M3 byte per dim (no codebook, no norm, the query
 // is not rotated); record D + D/2 bytes (SoA; two metadata fields: V scale, V zero) or a
 // D + D/2 + 4 byte slot (AoS: V scale and zero after the V codes).
@@ -78,6 +98,9 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
         acc[h][0] = acc[h][1] = 0.f;
     }
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
+    // SoA record sizes (128, 192, 112, 96 bytes) are multiples of 16 and the cache is 16-byte
+    // aligned, so with a 16-byte block stride every record starts 16-byte aligned
+    const bool a16 = LAYOUT == 0 && (block_stride & 15) == 0;
 
     for (int t0 = r.start; t0 < r.end; t0 += kWave) {
         const int t = t0 + lane;
@@ -141,10 +164,9 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
             s[h] = 0.f;
         float csq = 0.f;
         if constexpr (KB > 0) {
-            uint32_t kw[4 * KB];
-#pragma unroll
-            for (int w = 0; w < 4 * KB; ++w)
-                kw[w] = load_u32_a2(kp + 4 * w);
+            uint32_t kw[4 * KB], vw[4 * VB];
+            load_words(kw, kp, a16);
+            load_words(vw, vp, a16);
 #pragma unroll
             for (int d = 0; d < kHeadDim; ++d) {
                 const float c = lut[code_at<KB>(kw, d)];
@@ -156,10 +178,14 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
             }
 #pragma unroll
             for (int w = 0; w < 4 * VB; ++w)
-                vstage[lane][w] = load_u32_a2(vp + 4 * w);
+                vstage[lane][w] = vw[w];
         } else if constexpr (KF8) {
+            uint32_t kw[kHeadDim / 4], vw[kHalfD / 4];
+            load_words(kw, kp, a16);
+            load_words(vw, vp, a16);
+#pragma unroll
             for (int w = 0; w < kHeadDim / 4; ++w) {
-                const uint32_t word = load_u32_a2(kp + 4 * w);
+                const uint32_t word = kw[w];
                 const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, false);
                 const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, true);
                 const float k4[4] = {lo[0], lo[1], hi[0], hi[1]};
@@ -169,11 +195,16 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
                     for (int h = 0; h < G; ++h)
                         s[h] += qs[h][4 * w + n] * k4[n];
             }
+#pragma unroll
             for (int w = 0; w < kHalfD / 4; ++w)
-                vstage[lane][w] = load_u32_a2(vp + 4 * w);
+                vstage[lane][w] = vw[w];
         } else {
+            uint32_t kw[kHalfD / 4], vw[kHalfD / 4];
+            load_words(kw, kp, a16);
+            load_words(vw, vp, a16);
+#pragma unroll
             for (int w = 0; w < kHalfD / 4; ++w) {
-                const uint32_t word = load_u32_a2(kp + 4 * w);
+                const uint32_t word = kw[w];
 #pragma unroll
                 for (int n = 0; n < 8; ++n) {
                     const float c = lut[(word >> (4 * n)) & 15u];
@@ -183,7 +214,7 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
                     for (int h = 0; h < G; ++h)
                         s[h] += qs[h][8 * w + n] * c;
                 }
-                vstage[lane][w] = load_u32_a2(vp + 4 * w);
+                vstage[lane][w] = vw[w];
             }
         }
         float kscale = norm;
