@@ -133,7 +133,8 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
  * dim (record 128 K bytes | 64 V bytes, SoA metadata fields V scale and V zero; AoS slot
  * 196 bytes = K | V | scale | zero).  query is the unrotated query (fp32 [B, Hq, D]);
  * score = q.k * attn_scale.  Same mid_o contract, grid rule and sinks as tq4_stage1_ex;
- * runs on the VALU kernel.
+ * runs on the 16x16x32 MFMA kernel where it applies (GQA 4 or 8, power-of-two block_size
+ * >= 16, 16-byte block stride), else on the VALU kernel.
  * Replaces: _tq_decode_stage1 with KEY_FP8=1, reference/soa_decode_v1.py:213-230 (launch
  *           :519-606); the AoS kernel reference/aos_decode.py.
  */
@@ -141,6 +142,13 @@ int tq4_stage1_fp8(const float *query, const uint8_t *kv_cache, const int32_t *b
                    const int32_t *seq_lens, float *mid_o, int B, int Hq, int Hk, int D, int block_size,
                    int max_blocks_per_seq, int64_t cache_block_stride, int num_kv_splits, int layout,
                    float attn_scale, const float *sinks, tq4_stream_t stream);
+
+/* tq4_stage1_fp8 with the kernel choice of tq4_stage1_ex (AUTO, SIMPLE or XDL; MFMA is
+ * rejected).  Replaces: the same reference entry as tq4_stage1_fp8. */
+int tq4_stage1_fp8_ex(const float *query, const uint8_t *kv_cache, const int32_t *block_table,
+                      const int32_t *seq_lens, float *mid_o, int B, int Hq, int Hk, int D, int block_size,
+                      int max_blocks_per_seq, int64_t cache_block_stride, int num_kv_splits, int layout,
+                      float attn_scale, const float *sinks, int kernel, tq4_stream_t stream);
 
 /*
  * FP8-key preset writer: K cast to E4M3 (round to nearest even, saturating at +-448, NaN

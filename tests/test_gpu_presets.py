@@ -86,9 +86,9 @@ def test_store_preset_matches_oracle_writer(dev, preset, dtype, layout):
     assert np.array_equal(ref.reshape(-1)[~written], cache0.reshape(-1)[~written])
 
 
-def _table(rng, lens):
+def _table(rng, lens, bs=BS):
     lens = np.asarray(lens, np.int32)
-    need = (lens + BS - 1) // BS
+    need = (lens + bs - 1) // bs
     nb = int(need.sum()) + 2
     bt = np.zeros((len(lens), max(1, int(need.max()))), np.int32)
     perm = rng.permutation(nb).astype(np.int32)
@@ -99,16 +99,16 @@ def _table(rng, lens):
     return bt, lens, nb
 
 
-def _preset_cache(seed, lens, hk, kb, vb, layout):
+def _preset_cache(seed, lens, hk, kb, vb, layout, bs=BS):
     rng = np.random.default_rng(seed)
-    bt, lens, nb = _table(rng, lens)
-    n_tok = nb * BS
+    bt, lens, nb = _table(rng, lens, bs)
+    n_tok = nb * bs
     key = rng.standard_normal((n_tok, hk, D)).astype(np.float32)
     value = (rng.standard_normal((n_tok, hk, D)) * 0.8).astype(np.float32)
     cents, _ = _codebook(kb)
-    cache = np.zeros((nb, BS, hk, obits.slot_bytes(D, kb, vb)), np.uint8)
+    cache = np.zeros((nb, bs, hk, obits.slot_bytes(D, kb, vb)), np.uint8)
     obits.store(key, value, np.arange(n_tok), workloads.random_orthogonal(rng, D), cents, cache, kb, vb,
-                is_aos=layout == "aos")
+                block_size=bs, is_aos=layout == "aos")
     return bt, lens, cache, cents, rng
 
 
@@ -139,6 +139,20 @@ def test_stage1_preset_matches_oracle(dev, preset, layout, group):
     got = _stage1(dev, q, cache, bt, lens, cents, 8, kb, vb, layout)
     ref = ostage.stage1(q, cache, bt, lens, cents, 8, num_kv_heads=hk, is_aos=layout == "aos",
                         bits=preset)
+    _assert_parity(got, ref)
+
+
+@pytest.mark.parametrize("preset", PRESETS)
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_stage1_preset_block32_group2(dev, preset, layout):
+    """32-token KV blocks and GQA 2 (block stride 32 x Hk x slot)."""
+    kb, vb = preset
+    hk = 2
+    bt, lens, cache, cents, rng = _preset_cache(450, [33, 700, 64], hk, kb, vb, layout, bs=32)
+    q = rng.standard_normal((3, hk * 2, D)).astype(np.float32)
+    got = _stage1(dev, q, cache, bt, lens, cents, 5, kb, vb, layout)
+    ref = ostage.stage1(q, cache, bt, lens, cents, 5, num_kv_heads=hk, block_size=32,
+                        is_aos=layout == "aos", bits=preset)
     _assert_parity(got, ref)
 
 

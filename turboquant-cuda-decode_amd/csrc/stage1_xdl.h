@@ -38,6 +38,7 @@
 // Output: a finished split's rows go to an LDS image of the wave's part of mid_o, which
 // is written out as one contiguous run per head (see SpanCap).
 #pragma once
+#include <type_traits>
 #include "tq4_device.h"
 
 namespace tq4 {
@@ -148,23 +149,31 @@ struct LaneOffsets {
     int mf;          // SoA: bytes between the three metadata arrays
 };
 
-template <int LAYOUT, int G>
+// Bytes per (token, kv-head) record: SoA data record / AoS slot; KF8: the FP8-key preset
+// (128 K bytes | 64 V bytes, AoS + scale | zero).
+template <int LAYOUT, bool KF8> constexpr int record_bytes() {
+    return KF8 ? (LAYOUT == 0 ? kHeadDim + kHalfD : kHeadDim + kHalfD + 4) : (LAYOUT == 0 ? kSoaRecord : kAosSlot);
+}
+
+template <int LAYOUT, int G, bool KF8 = false>
 __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int hk, int block_size) {
     constexpr int TPL = G / 4;
     const int st = 4 * g + TPL * (n / G);  // first softmax token of the lane
-    const int rec = LAYOUT == 0 ? kSoaRecord : kAosSlot;
+    const int rec = record_bytes<LAYOUT, KF8>();
     LaneOffsets o;
     o.tok_stride = hk * rec;
     // K is loaded coalesced (each 16-lane row reads 4 whole 64-byte K records) and then
     // permuted across lanes into the MFMA layout (lane (n, g) = token n, bytes 16g ..).
     o.k = ((4 * g + (n >> 2)) * hk + kvh) * rec + 16 * (n & 3);
     o.kperm = 4 * (16 * (n >> 2) + 4 * (n & 3) + g);
-    o.v0 = (4 * g * hk + kvh) * rec + kHalfD + (LAYOUT == 0 ? 0 : 2) + 4 * n;
+    // KF8: the second 64 K bytes are loaded the same way from o.k + 64
+    o.v0 = (4 * g * hk + kvh) * rec + (KF8 ? kHeadDim : kHalfD + (LAYOUT == 0 ? 0 : 2)) + 4 * n;
     if (LAYOUT == 0) {
-        o.m = (kvh * 3 * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
+        // metadata fields: K norm, V scale, V zero (KF8: V scale, V zero)
+        o.m = (kvh * (KF8 ? 2 : 3) * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
         o.mf = block_size * 2;
     } else {
-        o.m = (st * hk + kvh) * kAosSlot;
+        o.m = (st * hk + kvh) * rec;
         o.mf = 0;
     }
     return o;
@@ -193,10 +202,40 @@ __device__ __forceinline__ void issue_k(RawK<LAYOUT> &t, __amdgpu_buffer_rsrc_t 
     t.k = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
 }
 
-template <int LAYOUT, int TPL>
+// FP8 keys: the two 64-byte halves of the 128 K bytes, each loaded as a 4-bit K record is.
+struct RawK8 {
+    uint4 k, k2;
+};
+__device__ __forceinline__ void issue_k(RawK8 &t, __amdgpu_buffer_rsrc_t rsrc, int doff, const LaneOffsets &o) {
+    t.k = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
+    t.k2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k + 64, doff, 0));
+}
+
+template <int LAYOUT, int TPL, bool KF8 = false>
 __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
                                         int moff, const LaneOffsets &o) {
-    if constexpr (LAYOUT == 0) {
+    if constexpr (KF8) {  // no K norm: fields V scale, V zero (SoA); scale | zero after V (AoS)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
+        if constexpr (LAYOUT == 0) {
+            if constexpr (TPL == 1) {
+                t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff, 0);
+                t.zero = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff + o.mf, 0);
+            } else {
+                t.scale = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m, moff, 0);
+                t.zero = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m, moff + o.mf, 0);
+            }
+            t.norm = 0x3C003C00u;  // f16 1.0 pair
+        } else {
+#pragma unroll
+            for (int j = 0; j < TPL; ++j) {
+                t.norm[j] = 0x3C00u;
+                t.scale_zero[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m + kHeadDim + kHalfD,
+                                                                       doff + j * o.tok_stride, 0);
+            }
+        }
+    } else if constexpr (LAYOUT == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
@@ -229,6 +268,15 @@ __device__ __forceinline__ uint4 decode_k(const RawK<LAYOUT> &t, const LaneOffse
                  (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.y),
                  (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.z),
                  (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)w.w)};
+}
+
+// FP8 keys: the lane's 32 K bytes (token n; bytes 16g .. 16g+15 of each 64-byte half).
+struct K8 {
+    uint4 a, b;
+};
+__device__ __forceinline__ K8 decode_k(const RawK8 &t, const LaneOffsets &o) {
+    const RawK<0> h0{t.k}, h1{t.k2};
+    return K8{decode_k<0>(h0, o), decode_k<0>(h1, o)};
 }
 
 // V dwords and metadata of one tile; metadata as f16 pairs (token j in half j).
@@ -283,12 +331,15 @@ struct LaneConst {
 // 2m, 2m+1 (dims d = 32g + 4m .. +3); its A slots are (c_hi, c_hi, c_lo, c_lo) of byte 2m
 // then of byte 2m+1, so bq[m] = (Q(2m), Q(2m), Q(2m+1), Q(2m+1)) with Q(b) the f16 pair
 // q_part(n)[head kvh*G + (n & (G-1))][32g + 2b, 32g + 2b + 1].
+// kf8: the lane-local dims of the FP8-key layout (dims 16g + 4m, m < 4; 64 + 16g + 4(m - 4)).
 __device__ __forceinline__ void load_q_rows(float4 (&qx)[8], const float *__restrict__ q_rot, int64_t head_row,
-                                            int g) {
-    const float *qp = q_rot + head_row * kHeadDim + 32 * g;
+                                            int g, bool kf8 = false) {
+    const float *qr = q_rot + head_row * kHeadDim;
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
-        qx[m] = *reinterpret_cast<const float4 *>(qp + 4 * m);
+    for (int m = 0; m < 8; ++m) {
+        const int d = kf8 ? (m < 4 ? 16 * g + 4 * m : 64 + 16 * g + 4 * (m - 4)) : 32 * g + 4 * m;
+        qx[m] = *reinterpret_cast<const float4 *>(qr + d);
+    }
 }
 __device__ __forceinline__ void q_operands(half8 (&bq)[8], const float4 (&qx)[8], int n, float scale) {
     const bool lo = n >= 8;
@@ -333,6 +384,23 @@ __device__ __forceinline__ KOps lookup_tile(const uint4 &k, const uint32_t *ktab
         }
         r.csq = fmaf(2.f, hl, hh);
     }
+    return r;
+}
+
+// FP8 keys: entry b = the f16 pair of the lane's K bytes 2b, 2b+1 (E4M3 -> f16 is exact), lo
+// part 0.  Lane-local dim i is dim 16g + i (i < 16) or 64 + 16g + i - 16 (the two halves).
+__device__ __forceinline__ KOps lookup_tile(const K8 &k, const uint32_t *) {
+    KOps r;
+    const uint32_t kw[8] = {k.a.x, k.a.y, k.a.z, k.a.w, k.b.x, k.b.y, k.b.z, k.b.w};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[w], false);  // bytes 0, 1
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[w], true);   // bytes 2, 3
+        r.e[2 * w].x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo[0], lo[1]));
+        r.e[2 * w + 1].x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(hi[0], hi[1]));
+        r.e[2 * w].y = r.e[2 * w + 1].y = 0u;
+    }
+    r.csq = 0.f;
     return r;
 }
 
@@ -653,7 +721,8 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
 //
 // FUSED (launched with one split per sequence and one wave per (sequence, kv-head)): the
 // wave writes the final output rows (out, out_dtype) and LSE instead of mid_o rows.
-template <int LAYOUT, int G, int WPE, bool FUSED>
+// KF8: the FP8-key preset (K one E4M3 byte per dim, no norm, the query not rotated).
+template <int LAYOUT, int G, int WPE, bool FUSED, bool KF8 = false>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
@@ -687,9 +756,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const int lane = threadIdx.x;
     // The pair-LUT rows and q do not depend on the sequence length: they go out first, the
     // K table and the q operands are built once the first tiles' loads are on their way.
-    const LutRows lut_rows = load_lut_rows(pair_lut, lane);
+    using RK = std::conditional_t<KF8, RawK8, RawK<LAYOUT>>;
+    LutRows lut_rows{};
+    if constexpr (!KF8)
+        lut_rows = load_lut_rows(pair_lut, lane);
     float4 q_rows[8];
-    load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + kvh * G + ((lane & 15) & (G - 1)), lane >> 4);
+    load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + kvh * G + ((lane & 15) & (G - 1)), lane >> 4, KF8);
     const int seq_len = seq_lens[b];
     // split partition: L = ceil(len / S); live splits are those with s * L < len
     const int split_len = (seq_len + num_splits - 1) / num_splits;
@@ -750,11 +822,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     total += tail;
     auto split_stop = [&](int s) { return ((split_tiles(s) + 1) & ~1) + (s == s_hi - 1 ? tail : 0); };
 
-    const LaneOffsets off = lane_offsets<LAYOUT, G>(lc.n, lc.g, kvh, num_kv_heads, block_size);
+    const LaneOffsets off = lane_offsets<LAYOUT, G, KF8>(lc.n, lc.g, kvh, num_kv_heads, block_size);
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
     const int tok0 = 4 * lc.g + TPL * (lc.n / G);  // the lane's first softmax token
     const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
-    const int rec = LAYOUT == 0 ? kSoaRecord : kAosSlot;
+    const int rec = record_bytes<LAYOUT, KF8>();
 
     int cur = s_lo;
     int img_s0 = s_lo;  // split of image slot 0
@@ -772,31 +844,38 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     };
     // The scheduling barriers keep the loads in program order, which is what lets each
     // wait count only the loads of later tiles.
-    auto issue_kpos = [&](RawK<LAYOUT> &r, uint32_t base_lo, uint32_t base_hi, int j) {
+    auto issue_kpos = [&](RK &r, uint32_t base_lo, uint32_t base_hi, int j) {
         const auto rsrc = rsrc_at(base_lo, base_hi, j);
         __builtin_amdgcn_sched_barrier(0);
-        issue_k<LAYOUT>(r, rsrc, 0, off);
+        if constexpr (KF8)
+            issue_k(r, rsrc, 0, off);
+        else
+            issue_k<LAYOUT>(r, rsrc, 0, off);
         __builtin_amdgcn_sched_barrier(0);
     };
     auto issue_vpos = [&](RawV<LAYOUT, TPL> &r, uint32_t base_lo, uint32_t base_hi, int moff_lane, int j) {
         const auto rsrc = rsrc_at(base_lo, base_hi, j);
         const int moff = LAYOUT == 0 ? __builtin_amdgcn_readlane(moff_lane, j & 63) : 0;
         __builtin_amdgcn_sched_barrier(0);
-        issue_v<LAYOUT, TPL>(r, rsrc, 0, moff, off);
+        issue_v<LAYOUT, TPL, KF8>(r, rsrc, 0, moff, off);
         __builtin_amdgcn_sched_barrier(0);
     };
 
     floatx4 sc;         // QK^T accumulator of the next tile
-    uint4 kn;           // K bytes of the next tile, in the MFMA layout
+    std::conditional_t<KF8, K8, uint4> kn;  // K bytes of the next tile, in the MFMA layout
     float csq_tot = 0;  // AoS: ||c[idx]||^2 of token n of that tile
     uint32_t aw[4];
 
     // Stage j: softmax of position j, then QK^T of position j + 1; odd stages also run
     // the PV of positions (j - 1, j).
     auto stage = [&](int k, const RawV<LAYOUT, TPL> &vprev, const RawV<LAYOUT, TPL> &vcur,
-                     const RawK<LAYOUT> &kafter, int mask_lane, int j) {
+                     const RK &kafter, int mask_lane, int j) {
         // K-table lookups of the next tile first: their latency runs under the softmax
-        const KOps e = lookup_tile<LAYOUT>(kn, ktab);
+        KOps e;
+        if constexpr (KF8)
+            e = lookup_tile(kn, ktab);
+        else
+            e = lookup_tile<LAYOUT>(kn, ktab);
         __builtin_amdgcn_sched_barrier(0);
         const TileV t = decode_v<LAYOUT, TPL>(vcur, off);
         const int t0 = 16 * __builtin_amdgcn_readlane(mask_lane, j & 63);
@@ -807,7 +886,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
 #pragma unroll
         for (int q = 0; q < TPL; ++q) {
             valid[q] = (uint32_t)(t0 + tok0 + q - cur_start) < (uint32_t)(cur_end - cur_start);
-            if constexpr (LAYOUT == 0) {
+            if constexpr (LAYOUT == 0 || KF8) {
                 nf[q] = half_at(t.norm, q);
             } else {
                 // ||c[idx]||^2 of token tok0 + q: totals sit in lanes n = token (any row)
@@ -824,10 +903,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         } else {
             sc = qk_tile(e, bq);
         }
-        if constexpr (LAYOUT == 1)
+        if constexpr (LAYOUT == 1 && !KF8)
             csq_tot = sum_xor16(sum_xor32(e.csq));
         // K bytes of position j + 2 into the MFMA layout (its load was issued 3 stages ago)
-        kn = decode_k<LAYOUT>(kafter, off);
+        if constexpr (KF8)
+            kn = decode_k(kafter, off);
+        else
+            kn = decode_k<LAYOUT>(kafter, off);
     };
 
     // Stream positions in chunks of 64 (one block-table entry per lane).  K loads of
@@ -838,7 +920,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     // chunk state: lane i holds stream position j0 + i's tile, mask and address
     int tile_lane = 0, mask_lane = 0, moff_lane = 0;
     uint32_t base_lo = 0, base_hi = 0;
-    RawK<LAYOUT> kr[RING];
+    RK kr[RING];
     RawV<LAYOUT, TPL> vr[RING];
     // Lane tables of chunk [j0, j0 + 64) and the ring's first loads.
     auto open_chunk = [&](int j0, int nchunk, int last) {
@@ -865,7 +947,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                                (uint64_t)(toff * num_kv_heads * rec);
             base_lo = (uint32_t)a;
             base_hi = (uint32_t)(a >> 32);
-            moff_lane = (block_size - toff) * num_kv_heads * kSoaRecord + toff * 2;
+            moff_lane = (block_size - toff) * num_kv_heads * rec + toff * 2;
         }
 #pragma unroll
         for (int k = 0; k < RING; ++k) {
@@ -876,7 +958,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
 
     // The first chunk's loads go out before the K table and the q operands are built.
     open_chunk(0, min(64, total), min(64, total) - 1);
-    build_key_table<LAYOUT>(ktab, lut_rows, lane);
+    if constexpr (!KF8)
+        build_key_table<LAYOUT>(ktab, lut_rows, lane);
     q_operands(bq, q_rows, lc.n, score_scale_log2);
     // one wave: its LDS writes complete before its later LDS reads; only the compiler must
     // keep the table lookups after the build
@@ -888,7 +971,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         const int last = j0 + nchunk - 1;
         if (j0 > 0)
             open_chunk(j0, nchunk, last);
-        {
+        if constexpr (KF8) {
+            sc = qk_tile(lookup_tile(decode_k(kr[0], off), ktab), bq);
+            kn = decode_k(kr[1], off);
+        } else {
             const KOps e = lookup_tile<LAYOUT>(decode_k<LAYOUT>(kr[0], off), ktab);
             sc = qk_tile(e, bq);
             if constexpr (LAYOUT == 1)

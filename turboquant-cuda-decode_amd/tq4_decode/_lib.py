@@ -25,6 +25,7 @@ EXPORTS = (
     "tq4_full_decode",
     "tq4_store",
     "tq4_stage1_fp8",
+    "tq4_stage1_fp8_ex",
     "tq4_store_fp8",
     "tq4_stage1_preset",
     "tq4_store_preset",
@@ -50,6 +51,7 @@ _SIGS = {
     "tq4_time_next_launch": [_p, _p],
     "tq4_stage1_fp8": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _p],
     "tq4_store_fp8": [_p, _p, _i, _p, _p, _i, _i, _i, _i, _i64, _i, _p],
+    "tq4_stage1_fp8_ex": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _i, _p],
     "tq4_stage1_preset": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _i,
                           _i, _p],
     "tq4_store_preset": [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _i, _i, _p],

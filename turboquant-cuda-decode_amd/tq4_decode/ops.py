@@ -200,9 +200,10 @@ def store(key, value, kv_cache, slot_mapping, rotation_t, midpoints, centroids=N
 
 
 def stage1_fp8(query, kv_cache, block_table, seq_lens, mid_o=None, *, num_kv_splits=None,
-               layout="soa", attn_scale=None, sinks=None):
+               layout="soa", attn_scale=None, sinks=None, kernel="auto"):
     """Stage1 of the FP8-key preset (``turboquant_k8v4``): ``query`` fp32 ``[B, Hq, D]``
-    (not rotated), K one E4M3 byte per dim; returns ``mid_o [B, Hq, S, D+1]``."""
+    (not rotated), K one E4M3 byte per dim; returns ``mid_o [B, Hq, S, D+1]``.  ``kernel``:
+    "auto" (16x16x32 MFMA where it applies, else VALU), "xdl" or "simple"."""
     for t, n, dt in ((query, "query", torch.float32), (kv_cache, "kv_cache", torch.uint8),
                      (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32)):
         _check_tensor(t, n, dt)
@@ -224,10 +225,12 @@ def stage1_fp8(query, kv_cache, block_table, seq_lens, mid_o=None, *, num_kv_spl
     devs = {t.device for t in (query, kv_cache, block_table, seq_lens, mid_o)}
     _require(len(devs) == 1, "all tensors must be on the same device")
     scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
-    rc = _lib.load().tq4_stage1_fp8(
+    _require(kernel in ("auto", "xdl", "simple"), "kernel must be auto, xdl or simple")
+    rc = _lib.load().tq4_stage1_fp8_ex(
         query.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
         mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), kv_cache.stride(0), S,
-        _layout_id(layout), scale, _check_sinks(sinks, Hq, query.device), _stream(query.device))
+        _layout_id(layout), scale, _check_sinks(sinks, Hq, query.device), KERNELS[kernel],
+        _stream(query.device))
     _lib.check(rc, "tq4_stage1_fp8")
     return mid_o
 
