@@ -138,6 +138,14 @@ __device__ __forceinline__ void build_key_table(uint32_t *tbl, const LutRows &v,
     }
 }
 
+// 3-bit keys: entry e = a | b << 3 holds ((c_hi[a], c_hi[b]), (c_lo[a], c_lo[b])) -- the
+// codes of a dim pair are 6 consecutive bits; one entry per lane (centroids [8]).
+__device__ __forceinline__ void build_key_table3(uint32_t *tbl, const float *centroids, int lane) {
+    const uint32_t pa = split_f16(centroids[lane & 7]), pb = split_f16(centroids[lane >> 3]);
+    tbl[2 * lane] = (pa & 0xFFFFu) | (pb << 16);
+    tbl[2 * lane + 1] = (pa >> 16) | (pb & 0xFFFF0000u);
+}
+
 // Per-lane byte offsets inside a KV block (fixed for a kernel instance); steps that are
 // the same for every lane travel in the loads' scalar offsets.
 struct LaneOffsets {
@@ -151,23 +159,34 @@ struct LaneOffsets {
 
 // Bytes per (token, kv-head) record: SoA data record / AoS slot; KF8: the FP8-key preset
 // (128 K bytes | 64 V bytes, AoS + scale | zero).
-template <int LAYOUT, bool KF8> constexpr int record_bytes() {
-    return KF8 ? (LAYOUT == 0 ? kHeadDim + kHalfD : kHeadDim + kHalfD + 4) : (LAYOUT == 0 ? kSoaRecord : kAosSlot);
+// KB3: 3-bit keys, 4-bit values (turboquant_k3v4_nc): 48 K bytes | 64 V bytes (SoA), AoS
+// K | norm | V | scale | zero = 118 bytes.
+constexpr int kK3Bytes = kHeadDim * 3 / 8;
+template <int LAYOUT, bool KF8, bool KB3 = false> constexpr int record_bytes() {
+    return KF8   ? (LAYOUT == 0 ? kHeadDim + kHalfD : kHeadDim + kHalfD + 4)
+           : KB3 ? (LAYOUT == 0 ? kK3Bytes + kHalfD : kK3Bytes + kHalfD + 6)
+                 : (LAYOUT == 0 ? kSoaRecord : kAosSlot);
+}
+// Byte offset of the V codes in a record.
+template <int LAYOUT, bool KF8, bool KB3 = false> constexpr int v_offset() {
+    return KF8 ? kHeadDim : (KB3 ? kK3Bytes : kHalfD) + (LAYOUT == 0 ? 0 : 2);
 }
 
-template <int LAYOUT, int G, bool KF8 = false>
+template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false>
 __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int hk, int block_size) {
     constexpr int TPL = G / 4;
     const int st = 4 * g + TPL * (n / G);  // first softmax token of the lane
-    const int rec = record_bytes<LAYOUT, KF8>();
+    const int rec = record_bytes<LAYOUT, KF8, KB3>();
     LaneOffsets o;
     o.tok_stride = hk * rec;
     // K is loaded coalesced (each 16-lane row reads 4 whole 64-byte K records) and then
     // permuted across lanes into the MFMA layout (lane (n, g) = token n, bytes 16g ..).
     o.k = ((4 * g + (n >> 2)) * hk + kvh) * rec + 16 * (n & 3);
+    if (KB3)  // 3-bit keys: lane (n, g) loads its own 12 bytes, token n, bytes 12g .. 12g+11
+        o.k = (n * hk + kvh) * rec + 12 * g;
     o.kperm = 4 * (16 * (n >> 2) + 4 * (n & 3) + g);
     // KF8: the second 64 K bytes are loaded the same way from o.k + 64
-    o.v0 = (4 * g * hk + kvh) * rec + (KF8 ? kHeadDim : kHalfD + (LAYOUT == 0 ? 0 : 2)) + 4 * n;
+    o.v0 = (4 * g * hk + kvh) * rec + v_offset<LAYOUT, KF8, KB3>() + 4 * n;
     if (LAYOUT == 0) {
         // metadata fields: K norm, V scale, V zero (KF8: V scale, V zero)
         o.m = (kvh * (KF8 ? 2 : 3) * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
@@ -211,7 +230,19 @@ __device__ __forceinline__ void issue_k(RawK8 &t, __amdgpu_buffer_rsrc_t rsrc, i
     t.k2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k + 64, doff, 0));
 }
 
-template <int LAYOUT, int TPL, bool KF8 = false>
+// 3-bit keys: the lane's 96 bits (dims 32g .. 32g+31, code d at bits 3(d - 32g)).
+struct RawK3 {
+    uint32_t w[3];
+};
+__device__ __forceinline__ void issue_k(RawK3 &t, __amdgpu_buffer_rsrc_t rsrc, int doff, const LaneOffsets &o) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(rsrc, o.k, doff, 0);
+    t.w[0] = v[0];
+    t.w[1] = v[1];
+    t.w[2] = v[2];
+}
+__device__ __forceinline__ RawK3 decode_k(const RawK3 &t, const LaneOffsets &) { return t; }
+
+template <int LAYOUT, int TPL, bool KF8 = false, bool KB3 = false>
 __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
                                         int moff, const LaneOffsets &o) {
     if constexpr (KF8) {  // no K norm: fields V scale, V zero (SoA); scale | zero after V (AoS)
@@ -252,10 +283,12 @@ __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rs
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
+        constexpr int kKb = KB3 ? kK3Bytes : kHalfD;  // K bytes before the norm
 #pragma unroll
         for (int j = 0; j < TPL; ++j) {
-            t.norm[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kHalfD, doff + j * o.tok_stride, 0);
-            t.scale_zero[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m + kHeadDim + 2, doff + j * o.tok_stride, 0);
+            t.norm[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kKb, doff + j * o.tok_stride, 0);
+            t.scale_zero[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m + kKb + 2 + kHalfD,
+                                                                   doff + j * o.tok_stride, 0);
         }
     }
 }
@@ -401,6 +434,35 @@ __device__ __forceinline__ KOps lookup_tile(const K8 &k, const uint32_t *) {
         r.e[2 * w].y = r.e[2 * w + 1].y = 0u;
     }
     r.csq = 0.f;
+    return r;
+}
+
+// 3-bit keys: entry b = the table entry of the lane's dims 2b, 2b+1 (bits 6b .. 6b+5 of its
+// 96 bits; pairs 5 and 10 straddle a word boundary); AoS sums ||c||^2 as the 4-bit path.
+template <int LAYOUT>
+__device__ __forceinline__ KOps lookup_tile(const RawK3 &k, const uint32_t *ktab) {
+    KOps r;
+    const uint2 *t2 = reinterpret_cast<const uint2 *>(ktab);
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+        const int bit = 6 * b, wi = bit >> 5, sh = bit & 31;
+        uint32_t v = k.w[wi] >> sh;
+        if (sh > 26)
+            v |= k.w[wi + 1] << (32 - sh);
+        r.e[b] = t2[v & 63u];
+    }
+    r.csq = 0.f;
+    if constexpr (LAYOUT == 1) {
+        float hh = 0.f, hl = 0.f;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const auto h = __builtin_bit_cast(__fp16 __attribute__((ext_vector_type(2))), r.e[b].x);
+            const auto l = __builtin_bit_cast(__fp16 __attribute__((ext_vector_type(2))), r.e[b].y);
+            hh = __builtin_amdgcn_fdot2(h, h, hh, false);
+            hl = __builtin_amdgcn_fdot2(h, l, hl, false);
+        }
+        r.csq = fmaf(2.f, hl, hh);
+    }
     return r;
 }
 
@@ -722,7 +784,8 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
 // FUSED (launched with one split per sequence and one wave per (sequence, kv-head)): the
 // wave writes the final output rows (out, out_dtype) and LSE instead of mid_o rows.
 // KF8: the FP8-key preset (K one E4M3 byte per dim, no norm, the query not rotated).
-template <int LAYOUT, int G, int WPE, bool FUSED, bool KF8 = false>
+// KB3: the 3-bit-key / 4-bit-value preset (pair_lut then holds the 8 centroids).
+template <int LAYOUT, int G, int WPE, bool FUSED, bool KF8 = false, bool KB3 = false>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
@@ -756,9 +819,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const int lane = threadIdx.x;
     // The pair-LUT rows and q do not depend on the sequence length: they go out first, the
     // K table and the q operands are built once the first tiles' loads are on their way.
-    using RK = std::conditional_t<KF8, RawK8, RawK<LAYOUT>>;
+    static_assert(!(KF8 && KB3), "one key format");
+    using RK = std::conditional_t<KF8, RawK8, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>;
     LutRows lut_rows{};
-    if constexpr (!KF8)
+    if constexpr (!KF8 && !KB3)
         lut_rows = load_lut_rows(pair_lut, lane);
     float4 q_rows[8];
     load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + kvh * G + ((lane & 15) & (G - 1)), lane >> 4, KF8);
@@ -822,11 +886,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     total += tail;
     auto split_stop = [&](int s) { return ((split_tiles(s) + 1) & ~1) + (s == s_hi - 1 ? tail : 0); };
 
-    const LaneOffsets off = lane_offsets<LAYOUT, G, KF8>(lc.n, lc.g, kvh, num_kv_heads, block_size);
+    const LaneOffsets off = lane_offsets<LAYOUT, G, KF8, KB3>(lc.n, lc.g, kvh, num_kv_heads, block_size);
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
     const int tok0 = 4 * lc.g + TPL * (lc.n / G);  // the lane's first softmax token
     const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
-    const int rec = record_bytes<LAYOUT, KF8>();
+    const int rec = record_bytes<LAYOUT, KF8, KB3>();
 
     int cur = s_lo;
     int img_s0 = s_lo;  // split of image slot 0
@@ -847,7 +911,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     auto issue_kpos = [&](RK &r, uint32_t base_lo, uint32_t base_hi, int j) {
         const auto rsrc = rsrc_at(base_lo, base_hi, j);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (KF8)
+        if constexpr (KF8 || KB3)
             issue_k(r, rsrc, 0, off);
         else
             issue_k<LAYOUT>(r, rsrc, 0, off);
@@ -857,12 +921,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         const auto rsrc = rsrc_at(base_lo, base_hi, j);
         const int moff = LAYOUT == 0 ? __builtin_amdgcn_readlane(moff_lane, j & 63) : 0;
         __builtin_amdgcn_sched_barrier(0);
-        issue_v<LAYOUT, TPL, KF8>(r, rsrc, 0, moff, off);
+        issue_v<LAYOUT, TPL, KF8, KB3>(r, rsrc, 0, moff, off);
         __builtin_amdgcn_sched_barrier(0);
     };
 
     floatx4 sc;         // QK^T accumulator of the next tile
-    std::conditional_t<KF8, K8, uint4> kn;  // K bytes of the next tile, in the MFMA layout
+    std::conditional_t<KF8, K8, std::conditional_t<KB3, RawK3, uint4>> kn;  // K bytes of the next tile, in the MFMA layout
     float csq_tot = 0;  // AoS: ||c[idx]||^2 of token n of that tile
     uint32_t aw[4];
 
@@ -906,7 +970,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         if constexpr (LAYOUT == 1 && !KF8)
             csq_tot = sum_xor16(sum_xor32(e.csq));
         // K bytes of position j + 2 into the MFMA layout (its load was issued 3 stages ago)
-        if constexpr (KF8)
+        if constexpr (KF8 || KB3)
             kn = decode_k(kafter, off);
         else
             kn = decode_k<LAYOUT>(kafter, off);
@@ -958,7 +1022,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
 
     // The first chunk's loads go out before the K table and the q operands are built.
     open_chunk(0, min(64, total), min(64, total) - 1);
-    if constexpr (!KF8)
+    if constexpr (KB3)
+        build_key_table3(ktab, pair_lut, lane);
+    else if constexpr (!KF8)
         build_key_table<LAYOUT>(ktab, lut_rows, lane);
     q_operands(bq, q_rows, lc.n, score_scale_log2);
     // one wave: its LDS writes complete before its later LDS reads; only the compiler must
@@ -974,6 +1040,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         if constexpr (KF8) {
             sc = qk_tile(lookup_tile(decode_k(kr[0], off), ktab), bq);
             kn = decode_k(kr[1], off);
+        } else if constexpr (KB3) {
+            const KOps e = lookup_tile<LAYOUT>(kr[0], ktab);
+            sc = qk_tile(e, bq);
+            if constexpr (LAYOUT == 1)
+                csq_tot = sum_xor16(sum_xor32(e.csq));
+            kn = kr[1];
         } else {
             const KOps e = lookup_tile<LAYOUT>(decode_k<LAYOUT>(kr[0], off), ktab);
             sc = qk_tile(e, bq);

@@ -202,19 +202,24 @@ template <int LAYOUT, int G> constexpr int xdl_waves_per_simd() {
     return LAYOUT == 0 && G == 4 ? TQ4_XDL_WAVES_PER_SIMD : 2;
 }
 
-template <int LAYOUT, int G, bool KF8 = false> int xdl_waves(const Stage1Args &a) {
+template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false> int xdl_waves(const Stage1Args &a) {
     static int slots = 0;
-    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>(), false, KF8>;
+    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>(), false, KF8, KB3>;
     return waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots);
 }
 
 template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
     constexpr int wpe = xdl_waves_per_simd<LAYOUT, G>();
-    const dim3 grid(a.Hk, a.key_fp8 ? xdl_waves<LAYOUT, G, true>(a) : xdl_waves<LAYOUT, G>(a), a.B);
+    const bool kb3 = a.key_bits == 3;
+    const dim3 grid(a.Hk,
+                    a.key_fp8 ? xdl_waves<LAYOUT, G, true>(a) : (kb3 ? xdl_waves<LAYOUT, G, false, true>(a) : xdl_waves<LAYOUT, G>(a)),
+                    a.B);
     auto kernel = a.out ? &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, true>
                         : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false>;
     if (a.key_fp8)  // never fused: the FP8-key decode runs Stage2 itself
         kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, true>;
+    else if (kb3)  // 3-bit keys, 4-bit values; never fused
+        kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, false, true>;
     launch(kernel, grid, dim3(tq4::kWave), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
            a.mid_o, a.sinks, a.out, a.out_dtype, a.lse, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks,
            a.stride, a.S, a.scale * tq4::kLog2e);
@@ -283,10 +288,17 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: FP8 keys run on the 16x16x32 or the VALU kernel");
     if (a.key_fp8 && a.out)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: no fused Stage2 for FP8 keys");
-    if (a.key_bits > 0 && kernel != TQ4_KERNEL_AUTO && kernel != TQ4_KERNEL_SIMPLE)
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_preset: the bit-width presets run on the VALU kernel");
+    // the bit-width presets: 3-bit K / 4-bit V also on the 16x16x32 kernel, the others VALU
+    const bool preset_xdl = a.key_bits == 3 && a.value_bits == 4;
+    if (a.key_bits > 0 && kernel != TQ4_KERNEL_AUTO && kernel != TQ4_KERNEL_SIMPLE &&
+        !(preset_xdl && kernel == TQ4_KERNEL_XDL))
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_preset: key/value bits %d/%d run on the VALU kernel%s",
+                    a.key_bits, a.value_bits, preset_xdl ? " or the 16x16x32 kernel" : "");
+    if (a.key_bits > 0 && a.out)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_preset: no fused Stage2 for the bit-width presets");
     if (kernel == TQ4_KERNEL_AUTO)
-        kernel = a.key_bits > 0 ? TQ4_KERNEL_SIMPLE : (mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE);
+        kernel = (a.key_bits > 0 && !preset_xdl) ? TQ4_KERNEL_SIMPLE
+                                                 : (mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE);
     if (kernel == TQ4_KERNEL_MFMA && a.sinks)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_ex: sinks need the XDL or the VALU kernel");
     if (kernel == TQ4_KERNEL_MFMA)
@@ -364,7 +376,7 @@ int tq4_time_next_launch(void *start_event, void *stop_event) {
     return ok();
 }
 
-int tq4_abi_version(void) { return 103; }
+int tq4_abi_version(void) { return 104; }
 
 const char *tq4_last_error(void) { return g_err; }
 
@@ -409,11 +421,12 @@ int tq4_stage1_fp8(const float *query, const uint8_t *kv_cache, const int32_t *b
                              sinks, TQ4_KERNEL_AUTO, stream);
 }
 
-int tq4_stage1_preset(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
-                      const int32_t *seq_lens, const float *centroids, float *mid_o, int B, int Hq,
-                      int Hk, int D, int block_size, int max_blocks_per_seq,
-                      int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
-                      const float *sinks, int key_bits, int value_bits, tq4_stream_t stream) {
+int tq4_stage1_preset_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+                         const int32_t *seq_lens, const float *centroids, float *mid_o, int B, int Hq,
+                         int Hk, int D, int block_size, int max_blocks_per_seq,
+                         int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+                         const float *sinks, int key_bits, int value_bits, int kernel,
+                         tq4_stream_t stream) {
     if (!preset_supported(key_bits, value_bits))
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_preset: key_bits / value_bits %d / %d unsupported "
                                        "(4/4, 3/4, 3/3)", key_bits, value_bits);
@@ -422,7 +435,17 @@ int tq4_stage1_preset(const float *q_rot, const uint8_t *kv_cache, const int32_t
                  attn_scale, sinks};
     a.key_bits = key_bits;
     a.value_bits = value_bits;
-    return run_stage1(a, TQ4_KERNEL_SIMPLE, reinterpret_cast<hipStream_t>(stream));
+    return run_stage1(a, kernel, reinterpret_cast<hipStream_t>(stream));
+}
+
+int tq4_stage1_preset(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
+                      const int32_t *seq_lens, const float *centroids, float *mid_o, int B, int Hq,
+                      int Hk, int D, int block_size, int max_blocks_per_seq,
+                      int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
+                      const float *sinks, int key_bits, int value_bits, tq4_stream_t stream) {
+    return tq4_stage1_preset_ex(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o, B, Hq, Hk, D,
+                                block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
+                                attn_scale, sinks, key_bits, value_bits, TQ4_KERNEL_AUTO, stream);
 }
 
 int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_dtype,

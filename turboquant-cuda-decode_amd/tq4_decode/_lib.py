@@ -28,6 +28,7 @@ EXPORTS = (
     "tq4_stage1_fp8_ex",
     "tq4_store_fp8",
     "tq4_stage1_preset",
+    "tq4_stage1_preset_ex",
     "tq4_store_preset",
     "tq4_last_error",
     "tq4_abi_version",
@@ -54,6 +55,8 @@ _SIGS = {
     "tq4_stage1_fp8_ex": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _i, _p],
     "tq4_stage1_preset": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _i,
                           _i, _p],
+    "tq4_stage1_preset_ex": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i, _i, _f, _p, _i,
+                             _i, _i, _p],
     "tq4_store_preset": [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _i, _i, _p],
 }
 

@@ -262,10 +262,12 @@ PRESETS = ((4, 4), (3, 4), (3, 3))  # (key bits, value bits) of the MSE-key pres
 
 
 def stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o=None, *, key_bits,
-                  value_bits, num_kv_splits=None, layout="soa", attn_scale=None, sinks=None):
+                  value_bits, num_kv_splits=None, layout="soa", attn_scale=None, sinks=None,
+                  kernel="auto"):
     """Stage1 of the bit-width presets (``turboquant_k3v4_nc``: 3/4, ``turboquant_3bit_nc``:
     3/3, and 4/4) on the VALU kernel: ``q_rot`` fp32 ``[B, Hq, D]``, ``centroids`` the
-    ``2^key_bits`` Lloyd-Max centroids; returns ``mid_o [B, Hq, S, D+1]``."""
+    ``2^key_bits`` Lloyd-Max centroids; returns ``mid_o [B, Hq, S, D+1]``.  ``kernel``:
+    "auto" (3/4 on the 16x16x32 MFMA kernel where it applies), "xdl" (3/4) or "simple"."""
     _require((key_bits, value_bits) in PRESETS, f"key/value bits must be one of {PRESETS}")
     for t, n, dt in ((q_rot, "q_rot", torch.float32), (kv_cache, "kv_cache", torch.uint8),
                      (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
@@ -291,11 +293,12 @@ def stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o=None,
     devs = {t.device for t in (q_rot, kv_cache, block_table, seq_lens, centroids, mid_o)}
     _require(len(devs) == 1, "all tensors must be on the same device")
     scale = 1.0 / math.sqrt(D) if attn_scale is None else float(attn_scale)
-    rc = _lib.load().tq4_stage1_preset(
+    _require(kernel in ("auto", "xdl", "simple"), "kernel must be auto, xdl or simple")
+    rc = _lib.load().tq4_stage1_preset_ex(
         q_rot.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
         centroids.data_ptr(), mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1),
         kv_cache.stride(0), S, _layout_id(layout), scale, _check_sinks(sinks, Hq, q_rot.device),
-        key_bits, value_bits, _stream(q_rot.device))
+        key_bits, value_bits, KERNELS[kernel], _stream(q_rot.device))
     _lib.check(rc, "tq4_stage1_preset")
     return mid_o
 
