@@ -469,6 +469,9 @@ def main() -> int:
     if not args.no_variants:
         result["store"] = store_times(dev, flush, timer)
         result["full_decode"] = full_decode_time(dev, flush, timer)
+        # Stage1 of the other presets at the same B64 x 4096 shape (each in its own layout)
+        result["presets"] = {name: stage1_preset_time(dev, flush, timer, name, reps=30)
+                             for name in PRESET_WORKLOADS}
     if args.calibrate_copy:
         src = torch.empty(1 << 26, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
