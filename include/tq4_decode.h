@@ -168,7 +168,7 @@ int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *
  * fp16 metadata fields K norm (folded norm correction), V scale, V zero; AoS slot
  * K | fp16 norm | V | fp16 scale | fp16 zero padded to even (118 bytes for 3/4, 102 for 3/3).
  * centroids: the 2^key_bits Lloyd-Max centroids.  Same mid_o contract, grid rule and sinks
- * as tq4_stage1_ex; 3/4 runs on the 16x16x32 MFMA kernel where it applies (GQA 4 or 8,
+ * as tq4_stage1_ex; 3/4 and 3/3 run on the 16x16x32 MFMA kernel where it applies (GQA 4 or 8,
  * power-of-two block_size >= 16, 16-byte block stride), everything else on the VALU kernel.
  * Replaces: _tq_decode_stage1 with MSE_BITS = 3 / VQB = 3, reference/soa_decode_v1.py:122-132
  *           (3-bit K unpack) and :271-284 (3-bit V unpack); the AoS kernel
@@ -180,7 +180,7 @@ int tq4_stage1_preset(const float *q_rot, const uint8_t *kv_cache, const int32_t
                       int64_t cache_block_stride, int num_kv_splits, int layout, float attn_scale,
                       const float *sinks, int key_bits, int value_bits, tq4_stream_t stream);
 
-/* tq4_stage1_preset with the kernel choice of tq4_stage1_ex (AUTO, SIMPLE, or XDL for 3/4).
+/* tq4_stage1_preset with the kernel choice of tq4_stage1_ex (AUTO, SIMPLE, or XDL for 3/4, 3/3).
  * Replaces: the same reference entry as tq4_stage1_preset. */
 int tq4_stage1_preset_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
                          const int32_t *seq_lens, const float *centroids, float *mid_o, int B, int Hq,

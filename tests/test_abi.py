@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
                         text=True, check=True).stdout
     exported = set(re.findall(r" T (tq4_\w+)$", nm, re.M))
     assert set(declared()) <= exported
-    assert _lib.load().tq4_abi_version() == 104
+    assert _lib.load().tq4_abi_version() == 105
 
 
 def _stage1_call(**over):

@@ -239,21 +239,22 @@ def test_preset_store_then_decode_entry(dev, preset, layout):
             mse_bits=kb, key_packed_size=kps, value_quant_bits=7 - vb, norm_correction=True)
 
 
+@pytest.mark.parametrize("vb", [4, 3])
 @pytest.mark.parametrize("layout", ["soa", "aos"])
 @pytest.mark.parametrize("group", [4, 8])
-def test_stage1_k3v4_on_the_mfma_kernel(dev, layout, group):
-    """3-bit K / 4-bit V on the 16x16x32 kernel (the auto choice for GQA 4 / 8): many splits
-    per wave, a 4096-token sequence, empty and one-token sequences, sinks.  Bound 1e-4 x
-    max(1, max|ref|): the MFMA kernel carries the softmax weights as f16 hi + lo parts."""
+def test_stage1_k3_on_the_mfma_kernel(dev, layout, group, vb):
+    """3-bit K / 4- or 3-bit V on the 16x16x32 kernel (the auto choice for GQA 4 / 8): many
+    splits per wave, a 4096-token sequence, empty and one-token sequences, sinks.  Bound
+    1e-4 x max(1, max|ref|): the MFMA kernel carries the softmax weights as f16 hi + lo parts."""
     hk = 8 // (group // 4)
-    bt, lens, cache, cents, rng = _preset_cache(460 + group, [4096, 0, 1, 333, 2049], hk, 3, 4, layout)
+    bt, lens, cache, cents, rng = _preset_cache(460 + group, [4096, 0, 1, 333, 2049], hk, 3, vb, layout)
     q = rng.standard_normal((len(lens), hk * group, D)).astype(np.float32)
     sinks = rng.normal(0, 2, hk * group).astype(np.float32)
     for sk in (None, sinks):
-        got = _stage1(dev, q, cache, bt, lens, cents, 32, 3, 4, layout, sinks=sk, kernel="xdl")
+        got = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, sinks=sk, kernel="xdl")
         ref = ostage.stage1(q, cache, bt, lens, cents, 32, num_kv_heads=hk, is_aos=layout == "aos",
-                            bits=(3, 4), sinks=sk)
+                            bits=(3, vb), sinks=sk)
         _assert_parity(got, ref, tol=1e-4 * max(1.0, float(np.nanmax(np.abs(ref)))))
-    auto = _stage1(dev, q, cache, bt, lens, cents, 32, 3, 4, layout, kernel="auto")
-    xdl = _stage1(dev, q, cache, bt, lens, cents, 32, 3, 4, layout, kernel="xdl")
+    auto = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, kernel="auto")
+    xdl = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, kernel="xdl")
     assert np.array_equal(auto, xdl, equal_nan=True), "auto runs the 16x16x32 kernel"

@@ -161,10 +161,11 @@ struct LaneOffsets {
 // (128 K bytes | 64 V bytes, AoS + scale | zero).
 // KB3: 3-bit keys, 4-bit values (turboquant_k3v4_nc): 48 K bytes | 64 V bytes (SoA), AoS
 // K | norm | V | scale | zero = 118 bytes.
+// V3 (with KB3): 3-bit values too (turboquant_3bit_nc): 48 K | 48 V bytes (SoA), AoS 102 bytes.
 constexpr int kK3Bytes = kHeadDim * 3 / 8;
-template <int LAYOUT, bool KF8, bool KB3 = false> constexpr int record_bytes() {
+template <int LAYOUT, bool KF8, bool KB3 = false, bool V3 = false> constexpr int record_bytes() {
     return KF8   ? (LAYOUT == 0 ? kHeadDim + kHalfD : kHeadDim + kHalfD + 4)
-           : KB3 ? (LAYOUT == 0 ? kK3Bytes + kHalfD : kK3Bytes + kHalfD + 6)
+           : KB3 ? (LAYOUT == 0 ? kK3Bytes + (V3 ? kK3Bytes : kHalfD) : kK3Bytes + (V3 ? kK3Bytes : kHalfD) + 6)
                  : (LAYOUT == 0 ? kSoaRecord : kAosSlot);
 }
 // Byte offset of the V codes in a record.
@@ -172,11 +173,11 @@ template <int LAYOUT, bool KF8, bool KB3 = false> constexpr int v_offset() {
     return KF8 ? kHeadDim : (KB3 ? kK3Bytes : kHalfD) + (LAYOUT == 0 ? 0 : 2);
 }
 
-template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false>
+template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false, bool V3 = false>
 __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int hk, int block_size) {
     constexpr int TPL = G / 4;
     const int st = 4 * g + TPL * (n / G);  // first softmax token of the lane
-    const int rec = record_bytes<LAYOUT, KF8, KB3>();
+    const int rec = record_bytes<LAYOUT, KF8, KB3, V3>();
     LaneOffsets o;
     o.tok_stride = hk * rec;
     // K is loaded coalesced (each 16-lane row reads 4 whole 64-byte K records) and then
@@ -186,7 +187,9 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int h
         o.k = (n * hk + kvh) * rec + 12 * g;
     o.kperm = 4 * (16 * (n >> 2) + 4 * (n & 3) + g);
     // KF8: the second 64 K bytes are loaded the same way from o.k + 64
-    o.v0 = (4 * g * hk + kvh) * rec + v_offset<LAYOUT, KF8, KB3>() + 4 * n;
+    // V3: the 3 bytes of dims 8n .. 8n+7 (a dword read; its fourth byte lies inside the
+    // record or, for n = 15, is the next record's / the metadata's first byte, masked off)
+    o.v0 = (4 * g * hk + kvh) * rec + v_offset<LAYOUT, KF8, KB3>() + (V3 ? 3 : 4) * n;
     if (LAYOUT == 0) {
         // metadata fields: K norm, V scale, V zero (KF8: V scale, V zero)
         o.m = (kvh * (KF8 ? 2 : 3) * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
@@ -242,7 +245,7 @@ __device__ __forceinline__ void issue_k(RawK3 &t, __amdgpu_buffer_rsrc_t rsrc, i
 }
 __device__ __forceinline__ RawK3 decode_k(const RawK3 &t, const LaneOffsets &) { return t; }
 
-template <int LAYOUT, int TPL, bool KF8 = false, bool KB3 = false>
+template <int LAYOUT, int TPL, bool KF8 = false, bool KB3 = false, bool V3 = false>
 __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
                                         int moff, const LaneOffsets &o) {
     if constexpr (KF8) {  // no K norm: fields V scale, V zero (SoA); scale | zero after V (AoS)
@@ -284,10 +287,11 @@ __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rs
         for (int i = 0; i < 4; ++i)
             t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
         constexpr int kKb = KB3 ? kK3Bytes : kHalfD;  // K bytes before the norm
+        constexpr int kVb = V3 ? kK3Bytes : kHalfD;   // V bytes before scale | zero
 #pragma unroll
         for (int j = 0; j < TPL; ++j) {
             t.norm[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m + kKb, doff + j * o.tok_stride, 0);
-            t.scale_zero[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m + kKb + 2 + kHalfD,
+            t.scale_zero[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.m + kKb + 2 + kVb,
                                                                    doff + j * o.tok_stride, 0);
         }
     }
@@ -484,11 +488,31 @@ __device__ __forceinline__ floatx4 qk_tile(const KOps &k, const half8 (&bq)[8]) 
 // PV of a pair of tiles (A operand aw, V dwords va / vb of tokens 4g .. 4g+3) interleaved
 // with QK^T of the next tile.  Accumulator 2m takes the even dim's codes (low nibbles),
 // accumulator 2m + 1 the whole bytes (lo + 16 * hi); the odd dim is recovered as
-// (acc[2m+1] - acc[2m]) / 16 when the split's rows are written.
+// (acc[2m+1] - acc[2m]) / 16 when the split's rows are written.  V3 (3-bit values, dims
+// 8n .. 8n+7 at bits 3(d - 8n) of the lane's dword): accumulator 2m takes the even dim's
+// codes, 2m + 1 the odd dim's, each a 3-bit field.
+template <bool V3 = false>
 __device__ __forceinline__ floatx4 pv_qk(floatx4 (&acc)[8], const uint32_t (&aw)[4], const uint32_t (&va)[4],
                                          const uint32_t (&vb)[4], const KOps &k, const half8 (&bq)[8]) {
     const half8 a = as_half8(aw[0], aw[1], aw[2], aw[3]);
     floatx4 h = {0.f, 0.f, 0.f, 0.f}, l = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (V3) {
+        // codes of two tokens' dwords x, y at bit b -> (code_x, code_y) as u16 slots
+        auto pair = [](uint32_t x, uint32_t y, int b) {
+            return ((x >> b) & 7u) | (((y >> b) & 7u) << 16);
+        };
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int be = 6 * m, bo = 6 * m + 3;
+            h = mfma(k_operand(k, 2 * m), bq[2 * m], h);
+            acc[2 * m] = mfma(a, as_half8(pair(va[0], va[1], be), pair(va[2], va[3], be), pair(vb[0], vb[1], be),
+                                          pair(vb[2], vb[3], be)), acc[2 * m]);
+            l = mfma(k_operand(k, 2 * m + 1), bq[2 * m + 1], l);
+            acc[2 * m + 1] = mfma(a, as_half8(pair(va[0], va[1], bo), pair(va[2], va[3], bo), pair(vb[0], vb[1], bo),
+                                              pair(vb[2], vb[3], bo)), acc[2 * m + 1]);
+        }
+        return h + l;
+    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         // byte m (dims 8n + 2m, 8n + 2m + 1) of two tokens' dwords -> (byte, 0, byte, 0)
@@ -665,7 +689,7 @@ template <int LAYOUT, int G, int WPE> struct SpanCap {
 
 // Rows of one split into image slot j: lane group g ends with heads hA, hA + 1 (see
 // rs_xor32), dims 8n .. 8n + 7; lanes 0 .. G-1 hold the LSE of head n.
-template <int G, class Cap>
+template <int G, class Cap, bool V3 = false>
 __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc)[8], const LaneConst &lc,
                                             float *img, int j) {
     const float lt = head_sum<G>(st.l);
@@ -679,13 +703,19 @@ __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc
     float oa[8], ob[8];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        // V codes entered as n * 2^-24; accumulator 2m + 1 holds (even + 16 * odd)
+        // V codes entered as n * 2^-24; accumulator 2m + 1 holds (even + 16 * odd), or (V3)
+        // the odd dim's codes
         const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
         const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
         oa[2 * m] = fmaf(xa, 16777216.0f, z_a) * inv_a;
         ob[2 * m] = fmaf(xb, 16777216.0f, z_b) * inv_b;
-        oa[2 * m + 1] = fmaf(ya - xa, 1048576.0f, z_a) * inv_a;
-        ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
+        if constexpr (V3) {
+            oa[2 * m + 1] = fmaf(ya, 16777216.0f, z_a) * inv_a;
+            ob[2 * m + 1] = fmaf(yb, 16777216.0f, z_b) * inv_b;
+        } else {
+            oa[2 * m + 1] = fmaf(ya - xa, 1048576.0f, z_a) * inv_a;
+            ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
+        }
     }
     if (G == 8 || (lc.g & 1) == 0) {
         float *ra = img + hA * Cap::head_floats + j * (kHeadDim + 1) + 8 * lc.n;
@@ -785,7 +815,7 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
 // wave writes the final output rows (out, out_dtype) and LSE instead of mid_o rows.
 // KF8: the FP8-key preset (K one E4M3 byte per dim, no norm, the query not rotated).
 // KB3: the 3-bit-key / 4-bit-value preset (pair_lut then holds the 8 centroids).
-template <int LAYOUT, int G, int WPE, bool FUSED, bool KF8 = false, bool KB3 = false>
+template <int LAYOUT, int G, int WPE, bool FUSED, bool KF8 = false, bool KB3 = false, bool V3 = false>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
@@ -820,6 +850,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     // The pair-LUT rows and q do not depend on the sequence length: they go out first, the
     // K table and the q operands are built once the first tiles' loads are on their way.
     static_assert(!(KF8 && KB3), "one key format");
+    static_assert(!V3 || (KB3 && !FUSED), "3-bit values come with 3-bit keys, not fused");
     using RK = std::conditional_t<KF8, RawK8, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>;
     LutRows lut_rows{};
     if constexpr (!KF8 && !KB3)
@@ -886,11 +917,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     total += tail;
     auto split_stop = [&](int s) { return ((split_tiles(s) + 1) & ~1) + (s == s_hi - 1 ? tail : 0); };
 
-    const LaneOffsets off = lane_offsets<LAYOUT, G, KF8, KB3>(lc.n, lc.g, kvh, num_kv_heads, block_size);
+    const LaneOffsets off = lane_offsets<LAYOUT, G, KF8, KB3, V3>(lc.n, lc.g, kvh, num_kv_heads, block_size);
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
     const int tok0 = 4 * lc.g + TPL * (lc.n / G);  // the lane's first softmax token
     const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
-    const int rec = record_bytes<LAYOUT, KF8, KB3>();
+    const int rec = record_bytes<LAYOUT, KF8, KB3, V3>();
 
     int cur = s_lo;
     int img_s0 = s_lo;  // split of image slot 0
@@ -921,7 +952,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         const auto rsrc = rsrc_at(base_lo, base_hi, j);
         const int moff = LAYOUT == 0 ? __builtin_amdgcn_readlane(moff_lane, j & 63) : 0;
         __builtin_amdgcn_sched_barrier(0);
-        issue_v<LAYOUT, TPL, KF8, KB3>(r, rsrc, 0, moff, off);
+        issue_v<LAYOUT, TPL, KF8, KB3, V3>(r, rsrc, 0, moff, off);
         __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -963,7 +994,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             softmax_tile<G, false>(dot, nf, t, st, acc, lc, boundary, valid, aw[0], aw[1], aw[0], aw[1]);
         if (k & 1) {
             const TileV ta = decode_v<LAYOUT, TPL>(vprev, off);
-            sc = pv_qk(acc, aw, ta.v, t.v, e, bq);
+            sc = pv_qk<V3>(acc, aw, ta.v, t.v, e, bq);
         } else {
             sc = qk_tile(e, bq);
         }
@@ -1066,7 +1097,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                     // a split ends after an odd stage (FUSED: the only split ends with the
                     // stream; its rows are written after the loop)
                     if (!FUSED && j + k + 1 == pos_base + cur_stop) {
-                        stash_split<G, Cap>(st, acc, lc, img, cur - img_s0);
+                        stash_split<G, Cap, V3>(st, acc, lc, img, cur - img_s0);
                         if (cur + 1 == s_hi || cur + 1 - img_s0 == Cap::splits) {
                             flush_splits<G, Cap>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
                             img_s0 = cur + 1;

@@ -202,24 +202,26 @@ template <int LAYOUT, int G> constexpr int xdl_waves_per_simd() {
     return LAYOUT == 0 && G == 4 ? TQ4_XDL_WAVES_PER_SIMD : 2;
 }
 
-template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false> int xdl_waves(const Stage1Args &a) {
+template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false, bool V3 = false> int xdl_waves(const Stage1Args &a) {
     static int slots = 0;
-    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>(), false, KF8, KB3>;
+    const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>(), false, KF8, KB3, V3>;
     return waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots);
 }
 
 template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
     constexpr int wpe = xdl_waves_per_simd<LAYOUT, G>();
-    const bool kb3 = a.key_bits == 3;
-    const dim3 grid(a.Hk,
-                    a.key_fp8 ? xdl_waves<LAYOUT, G, true>(a) : (kb3 ? xdl_waves<LAYOUT, G, false, true>(a) : xdl_waves<LAYOUT, G>(a)),
-                    a.B);
+    const bool kb3 = a.key_bits == 3, v3 = a.value_bits == 3;
+    const int waves = a.key_fp8 ? xdl_waves<LAYOUT, G, true>(a)
+                      : kb3     ? (v3 ? xdl_waves<LAYOUT, G, false, true, true>(a) : xdl_waves<LAYOUT, G, false, true>(a))
+                                : xdl_waves<LAYOUT, G>(a);
+    const dim3 grid(a.Hk, waves, a.B);
     auto kernel = a.out ? &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, true>
                         : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false>;
     if (a.key_fp8)  // never fused: the FP8-key decode runs Stage2 itself
         kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, true>;
-    else if (kb3)  // 3-bit keys, 4-bit values; never fused
-        kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, false, true>;
+    else if (kb3)  // 3-bit keys, 4- or 3-bit values; never fused
+        kernel = v3 ? &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, false, true, true>
+                    : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, false, true>;
     launch(kernel, grid, dim3(tq4::kWave), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
            a.mid_o, a.sinks, a.out, a.out_dtype, a.lse, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks,
            a.stride, a.S, a.scale * tq4::kLog2e);
@@ -288,8 +290,8 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: FP8 keys run on the 16x16x32 or the VALU kernel");
     if (a.key_fp8 && a.out)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: no fused Stage2 for FP8 keys");
-    // the bit-width presets: 3-bit K / 4-bit V also on the 16x16x32 kernel, the others VALU
-    const bool preset_xdl = a.key_bits == 3 && a.value_bits == 4;
+    // the bit-width presets: 3-bit K (4- or 3-bit V) also on the 16x16x32 kernel, 4/4 VALU
+    const bool preset_xdl = a.key_bits == 3;
     if (a.key_bits > 0 && kernel != TQ4_KERNEL_AUTO && kernel != TQ4_KERNEL_SIMPLE &&
         !(preset_xdl && kernel == TQ4_KERNEL_XDL))
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_preset: key/value bits %d/%d run on the VALU kernel%s",
@@ -376,7 +378,7 @@ int tq4_time_next_launch(void *start_event, void *stop_event) {
     return ok();
 }
 
-int tq4_abi_version(void) { return 104; }
+int tq4_abi_version(void) { return 105; }
 
 const char *tq4_last_error(void) { return g_err; }
 

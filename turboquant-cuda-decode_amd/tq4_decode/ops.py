@@ -267,7 +267,7 @@ def stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o=None,
     """Stage1 of the bit-width presets (``turboquant_k3v4_nc``: 3/4, ``turboquant_3bit_nc``:
     3/3, and 4/4) on the VALU kernel: ``q_rot`` fp32 ``[B, Hq, D]``, ``centroids`` the
     ``2^key_bits`` Lloyd-Max centroids; returns ``mid_o [B, Hq, S, D+1]``.  ``kernel``:
-    "auto" (3/4 on the 16x16x32 MFMA kernel where it applies), "xdl" (3/4) or "simple"."""
+    "auto" (3/4 and 3/3 on the 16x16x32 MFMA kernel where it applies), "xdl" or "simple"."""
     _require((key_bits, value_bits) in PRESETS, f"key/value bits must be one of {PRESETS}")
     for t, n, dt in ((q_rot, "q_rot", torch.float32), (kv_cache, "kv_cache", torch.uint8),
                      (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
