@@ -829,10 +829,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const int block_size = 1 << block_size_log2;
     int kvh = blockIdx.x, wid = blockIdx.y, b = blockIdx.z;
     const int nw = gridDim.y;
-    if constexpr (LAYOUT == 1) {
+    if constexpr (LAYOUT == 1 || KF8 || KB3) {
         // Workgroups are dealt to the XCDs round-robin by linear id (8 on gfx950), so with
-        // the plain map kv-head h runs on XCD h.  An AoS slot of kv-head h shares 128-byte
-        // lines with the slots of h - 1 and h + 1: the kv-heads of one (sequence, wave)
+        // the plain map kv-head h runs on XCD h.  An AoS slot (or a preset's SoA record of
+        // 192, 112 or 96 bytes) of kv-head h shares 128-byte lines with those of h - 1 and h + 1: the kv-heads of one (sequence, wave)
         // pair go to one XCD instead, so each line is fetched from HBM into one L2 (halves
         // the HBM reads).  A bijection of the grid whenever the pair count is a multiple of 8.
         constexpr int kXcds = 8;
