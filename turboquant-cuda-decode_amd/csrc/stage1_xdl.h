@@ -183,8 +183,13 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int h
     // K is loaded coalesced (each 16-lane row reads 4 whole 64-byte K records) and then
     // permuted across lanes into the MFMA layout (lane (n, g) = token n, bytes 16g ..).
     o.k = ((4 * g + (n >> 2)) * hk + kvh) * rec + 16 * (n & 3);
-    if (KB3)  // 3-bit keys: lane (n, g) loads its own 12 bytes, token n, bytes 12g .. 12g+11
-        o.k = (n * hk + kvh) * rec + 12 * g;
+    if (KB3) {
+        // 3-bit keys: lane 16g + n loads 12 bytes, chunk (n & 3) of token 4g + (n >> 2), so
+        // four consecutive lanes read one whole 48-byte K record; lane (n, g) then takes
+        // chunk g of token n (the codes of dims 32g .. 32g+31) from lane 4n + g
+        o.k = ((4 * g + (n >> 2)) * hk + kvh) * rec + 12 * (n & 3);
+        o.kperm = 4 * (4 * n + g);
+    }
     o.kperm = 4 * (16 * (n >> 2) + 4 * (n & 3) + g);
     // KF8: the second 64 K bytes are loaded the same way from o.k + 64
     // V3: the 3 bytes of dims 8n .. 8n+7 (a dword read; its fourth byte lies inside the
@@ -233,7 +238,8 @@ __device__ __forceinline__ void issue_k(RawK8 &t, __amdgpu_buffer_rsrc_t rsrc, i
     t.k2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k + 64, doff, 0));
 }
 
-// 3-bit keys: the lane's 96 bits (dims 32g .. 32g+31, code d at bits 3(d - 32g)).
+// 3-bit keys: 96 bits of one K record (after decode_k: the lane's dims 32g .. 32g+31, code d
+// at bits 3(d - 32g)).
 struct RawK3 {
     uint32_t w[3];
 };
@@ -243,7 +249,13 @@ __device__ __forceinline__ void issue_k(RawK3 &t, __amdgpu_buffer_rsrc_t rsrc, i
     t.w[1] = v[1];
     t.w[2] = v[2];
 }
-__device__ __forceinline__ RawK3 decode_k(const RawK3 &t, const LaneOffsets &) { return t; }
+__device__ __forceinline__ RawK3 decode_k(const RawK3 &t, const LaneOffsets &o) {
+    RawK3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        r.w[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(o.kperm, (int)t.w[i]);
+    return r;
+}
 
 template <int LAYOUT, int TPL, bool KF8 = false, bool KB3 = false, bool V3 = false>
 __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
@@ -1072,11 +1084,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             sc = qk_tile(lookup_tile(decode_k(kr[0], off), ktab), bq);
             kn = decode_k(kr[1], off);
         } else if constexpr (KB3) {
-            const KOps e = lookup_tile<LAYOUT>(kr[0], ktab);
+            const KOps e = lookup_tile<LAYOUT>(decode_k(kr[0], off), ktab);
             sc = qk_tile(e, bq);
             if constexpr (LAYOUT == 1)
                 csq_tot = sum_xor16(sum_xor32(e.csq));
-            kn = kr[1];
+            kn = decode_k(kr[1], off);
         } else {
             const KOps e = lookup_tile<LAYOUT>(decode_k<LAYOUT>(kr[0], off), ktab);
             sc = qk_tile(e, bq);
