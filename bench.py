@@ -122,17 +122,20 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
-def store_times(dev, flush, timer, reps=30, only=None):
-    """Cache writer (tq4_store, SoA, bf16 K/V, norm correction) cold, kernel duration: one
-    decode step (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  Bytes per (token,
-    kv-head): 2 x 256 read + 134 written, plus 4 of slot mapping per token."""
+def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4)):
+    """Cache writer (SoA, bf16 K/V, norm correction) cold, kernel duration: one decode step
+    (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  ``bits``: key / value bits
+    (4/4: tq4_store; 3/4 and 3/3: tq4_store_preset).  Bytes per (token, kv-head): 2 x 256
+    read + the slot written, plus 4 of slot mapping per token."""
     import numpy as np
     import torch
 
     from tq4_decode import codebook, ops, workloads
 
     rng = np.random.default_rng(7)
-    cents = codebook.centroids(128, 4)
+    kb, vb = bits
+    slot = ops.slot_bytes_preset(128, kb, vb)
+    cents = codebook.centroids(128, kb)
     mids = ((cents[:-1] + cents[1:]) * np.float32(0.5)).astype(np.float32)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     rot, c, m = t(workloads.random_orthogonal(rng, 128)), t(cents), t(mids)
@@ -143,20 +146,23 @@ def store_times(dev, flush, timer, reps=30, only=None):
         key = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
         val = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
         n_blocks = (n_tok + 15) // 16 + 4
-        cache = torch.zeros(n_blocks, 16, 8, 134, dtype=torch.uint8, device=dev)
+        cache = torch.zeros(n_blocks, 16, 8, slot, dtype=torch.uint8, device=dev)
         slots = torch.randperm(n_blocks * 16, device=dev)[:n_tok].to(torch.int32)
         times = []
         for i in range(reps + 3):
             flush.sum()
             a, b = timer.pair()
             timer.stamp_next_launch(a, b)  # the kernel's own start and end
-            ops.store(key, val, cache, slots, rot, m, c)
+            if bits == (4, 4):
+                ops.store(key, val, cache, slots, rot, m, c)
+            else:
+                ops.store_preset(key, val, cache, slots, rot, m, c, key_bits=kb, value_bits=vb)
             torch.cuda.synchronize()
             if i >= 3:
                 times.append(timer.elapsed_ms(a, b) * 1e3)
             timer.destroy(a, b)
         us = statistics.median(times)
-        nbytes = n_tok * 8 * (2 * 256 + 134) + n_tok * 4
+        nbytes = n_tok * 8 * (2 * 256 + slot) + n_tok * 4
         out[f"{name}_us"] = round(us, 2)
         out[f"{name}_GBps"] = round(nbytes / us / 1e3, 1)
     return out
@@ -316,9 +322,14 @@ def side_workload(args, dev) -> int:
         dtype = ("e4m3 K, 4-bit V" if preset == "fp8" else f"{preset[0]}-bit K, {preset[1]}-bit V") + ", f32 math"
     elif args.workload.startswith("store_"):
         size = args.workload[len("store_"):]
-        r = store_times(dev, flush, timer, reps=args.steps, only=size)
+        bits = (4, 4)
+        for tag, b in (("k3v4_", (3, 4)), ("3bit_", (3, 3))):
+            if size.startswith(tag):
+                size, bits = size[len(tag):], b
+        r = store_times(dev, flush, timer, reps=args.steps, only=size, bits=bits)
         us, gbs = r[f"{size}_us"], r[f"{size}_GBps"]
-        metric = f"cache writer (tq4_store, SoA, bf16 K/V, 8 kv-heads) {size}: GB/s"
+        entry = "tq4_store" if bits == (4, 4) else f"tq4_store_preset {bits[0]}/{bits[1]}"
+        metric = f"cache writer ({entry}, SoA, bf16 K/V, 8 kv-heads) {size}: GB/s"
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = "bf16 in, f32 math"
     else:
@@ -349,7 +360,7 @@ def main() -> int:
                     help="also run a 256 MiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--workload", default="stage1",
                     choices=["stage1", "store_decode_b64", "store_prefill_n8192", "full_decode_b256",
-                             *PRESET_WORKLOADS],
+                             "store_k3v4_prefill_n8192", "store_3bit_prefill_n8192", *PRESET_WORKLOADS],
                     help="stage1: the headline (default); the others time only that workload "
                          "(--steps cold launches) and print its own JSON line, e.g. for a profile")
     args = ap.parse_args()
