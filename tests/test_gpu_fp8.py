@@ -174,3 +174,25 @@ def test_stage1_fp8_xdl_long_and_ragged(dev, layout, group):
     ref = ostage.stage1(query, cache, w.block_table, w.seq_lens, None, 32, num_kv_heads=hk,
                         is_aos=layout == "aos", key_fp8=True)
     _assert_parity(got, ref)
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("bs", [32, 64])
+def test_stage1_fp8_xdl_larger_blocks(dev, layout, bs):
+    """The 16x16x32 kernel at 32 / 64-token KV blocks (piece and metadata offsets of the
+    192 / 196-byte records)."""
+    rng = np.random.default_rng(309 + bs)
+    lens = [130, 511, 64, 2000]
+    w = workloads.small(309, len(lens), lens, 8, block_size=bs)
+    nb = w.kv_cache.shape[0]
+    n_tok = nb * bs
+    key = (rng.standard_normal((n_tok, HK, D)) * 2).astype(np.float32)
+    value = rng.standard_normal((n_tok, HK, D)).astype(np.float32)
+    cache = np.zeros((nb, bs, HK, SLOT), np.uint8)
+    ostore.store_fp8(key, value, np.arange(n_tok, dtype=np.int32), cache, block_size=bs,
+                     is_aos=layout == "aos")
+    query = rng.standard_normal((len(lens), 32, D)).astype(np.float32)
+    got = _stage1(dev, w, cache, query, 8, layout, kernel="xdl")
+    ref = ostage.stage1(query, cache, w.block_table, w.seq_lens, None, 8, num_kv_heads=HK,
+                        block_size=bs, is_aos=layout == "aos", key_fp8=True)
+    _assert_parity(got, ref)

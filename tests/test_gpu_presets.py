@@ -258,3 +258,18 @@ def test_stage1_k3_on_the_mfma_kernel(dev, layout, group, vb):
     auto = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, kernel="auto")
     xdl = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, kernel="xdl")
     assert np.array_equal(auto, xdl, equal_nan=True), "auto runs the 16x16x32 kernel"
+
+
+@pytest.mark.parametrize("vb", [4, 3])
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("bs", [32, 64])
+def test_stage1_k3_mfma_larger_blocks(dev, layout, bs, vb):
+    """The 16x16x32 kernel at 32 / 64-token KV blocks (several 16-token pieces per block:
+    the piece and metadata offsets use the preset's record size)."""
+    hk = 8
+    bt, lens, cache, cents, rng = _preset_cache(470 + bs, [130, 511, 64, 2000], hk, 3, vb, layout, bs=bs)
+    q = rng.standard_normal((len(lens), hk * 4, D)).astype(np.float32)
+    got = _stage1(dev, q, cache, bt, lens, cents, 8, 3, vb, layout, kernel="xdl")
+    ref = ostage.stage1(q, cache, bt, lens, cents, 8, num_kv_heads=hk, block_size=bs,
+                        is_aos=layout == "aos", bits=(3, vb))
+    _assert_parity(got, ref, tol=1e-4 * max(1.0, float(np.nanmax(np.abs(ref)))))
