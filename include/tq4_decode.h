@@ -1,7 +1,9 @@
 /*
  * tq4_decode.h -- C ABI of the MI355X (gfx950) TurboQuant `turboquant_4bit_nc`
  * decode path: Stage1 split-KV attention over the 4-bit paged cache, the Stage2
- * split reduction, and the query-rotation / pair-LUT prologue of a full step.
+ * split reduction, and the query-rotation / pair-LUT prologue of a full step; the
+ * cache writers; and the other presets' Stage1 and writers (FP8 keys
+ * `turboquant_k8v4`, 3-bit keys `turboquant_k3v4_nc` / `turboquant_3bit_nc`).
  *
  * All pointers are device pointers; all calls are asynchronous on `stream` and
  * allocate nothing.  Every entry point returns 0 on success, otherwise a
