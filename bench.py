@@ -12,8 +12,13 @@ Prints ONE JSON line.  ``value`` is achieved HBM GB/s = algorithmic bytes per la
 mean launch time; ``roofline`` relates it to MI355X's 8 TB/s; ``cpu_baseline`` is the
 C oracle (a port of the reference Stage1 math) timed on this host's cores.
 
+Beside the headline: the other Stage1 workloads of the same kernel (ragged B64, GQA-8
+B8 x 32768), Stage2 at the headline shape, the reference-method warm number (100
+back-to-back launches), the cache writer, the full decode step, the presets, and the
+measured stream ceiling of this GPU (a device copy and a read-only sweep).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layout soa|aos]
-                       [--kernel auto|xdl|mfma|simple] [--no-cpu-baseline] [--calibrate-copy]
+                       [--kernel auto|xdl|simple] [--no-cpu-baseline] [--calibrate-copy]
 """
 from __future__ import annotations
 
@@ -261,6 +266,90 @@ def stage1_preset_time(dev, flush, timer, name, reps=30):
     return {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes}
 
 
+def stage1_workload_time(dev, flush, timer, w, reps=30):
+    """Stage1 (auto kernel, SoA) of another 4-bit workload, cold, kernel duration (median of
+    ``reps``); bytes as ``algorithmic_bytes``."""
+    import numpy as np
+    import torch
+
+    from tq4_decode import ops
+
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    q, c, bt, sl, lut = t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens), t(w.pair_lut)
+    mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
+    times = []
+    for i in range(reps + 3):
+        flush.sum()
+        a, b = timer.pair()
+        timer.stamp_next_launch(a, b)
+        ops.stage1(q, c, bt, sl, lut, mid)
+        torch.cuda.synchronize()
+        if i >= 3:
+            times.append(timer.elapsed_ms(a, b) * 1e3)
+        timer.destroy(a, b)
+    us = statistics.median(times)
+    nbytes = algorithmic_bytes(w)
+    gbs = nbytes / us / 1e3
+    return {"us": round(us, 2), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": nbytes}
+
+
+def stage2_time(dev, flush, timer, w, mid, reps=30):
+    """Stage2 over the headline's mid_o (B64 x 32 heads x 32 splits), fp32 output, cold,
+    kernel duration.  Bytes: the mid_o rows read, the output rows and LSE written, seq_lens."""
+    import numpy as np
+    import torch
+
+    from tq4_decode import ops
+
+    sl = torch.from_numpy(np.ascontiguousarray(w.seq_lens)).to(dev)
+    out = torch.empty(w.batch, w.num_q_heads, w.head_dim, device=dev)
+    lse = torch.empty(w.batch, w.num_q_heads, device=dev)
+    times = []
+    for i in range(reps + 3):
+        flush.sum()
+        a, b = timer.pair()
+        timer.stamp_next_launch(a, b)
+        ops.stage2(mid, sl, out, lse)
+        torch.cuda.synchronize()
+        if i >= 3:
+            times.append(timer.elapsed_ms(a, b) * 1e3)
+        timer.destroy(a, b)
+    us = statistics.median(times)
+    nbytes = mid.numel() * 4 + out.numel() * 4 + lse.numel() * 4 + w.seq_lens.nbytes
+    return {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes,
+            "shape": "B64 x 32 q-heads x 32 splits, fp32 out"}
+
+
+def stream_ceiling(dev, timer, reps=10):
+    """This GPU's streaming bandwidth, measured: a 2 x 1 GiB device copy (torch ``copy_``,
+    bytes read + written) and a read-only sweep of 2 GiB (torch ``sum``), median of ``reps``,
+    events around each launch (the 4 GiB working set is far beyond the Infinity Cache)."""
+    import torch
+
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev).uniform_()
+    dst = torch.empty_like(src)
+    big = torch.empty(1 << 29, dtype=torch.float32, device=dev).uniform_()
+    out = {}
+    for name, fn, nbytes in (("copy_GBps", lambda: dst.copy_(src), 2 * src.nbytes),
+                             ("read_GBps", lambda: big.sum(), big.nbytes)):
+        times = []
+        for i in range(reps + 2):
+            a, b = timer.pair()
+            timer.record(a)
+            fn()
+            timer.record(b)
+            torch.cuda.synchronize()
+            if i >= 2:
+                times.append(timer.elapsed_ms(a, b))
+            timer.destroy(a, b)
+        out[name] = round(nbytes / statistics.median(times) / 1e6, 1)
+    del src, dst, big
+    out["how"] = ("torch copy_ of 1 GiB (2 GiB moved) and torch sum over 2 GiB, events around "
+                  "the launch, median of %d" % reps)
+    return out
+
+
 def cpu_baseline(w, threads: int, repeats: int = 3):
     """The reference's fp32 Stage1 math in PyTorch on the host cores (the oracle's
     vectorized restatement of tools/cuda_v1_diagnostic.py:106-224), whole workload."""
@@ -353,7 +442,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layout", default="soa", choices=["soa", "aos"])
-    ap.add_argument("--kernel", default="auto", choices=["auto", "mfma", "simple", "xdl"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "simple", "xdl"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-variants", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -470,14 +559,23 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
     }
+    # the reference's method: 100 back-to-back launches (benchmarks/stage1.py:32-43); the
+    # 316 MB working set then partly stays in the 256 MB Infinity Cache
+    result["stage1_us_warm"] = round(warm_time(args.layout, args.kernel) * 1e3, 2)
     if not args.no_variants:
         var = {}
-        for layout, kernel in (("soa", "mfma"), ("aos", "xdl"), ("aos", "mfma"), ("soa", "simple")):
+        for layout, kernel in (("aos", "xdl"), ("soa", "simple")):
             vm = statistics.fmean(cold_times(layout, kernel, 50, 5))
             var[f"{layout}_{kernel}_cold_us"] = round(vm * 1e3, 2)
             var[f"{layout}_{kernel}_warm_us"] = round(warm_time(layout, kernel) * 1e3, 2)
         result["variants"] = var
-    if not args.no_variants:
+        launch("soa", "xdl")  # mid_o of the headline for Stage2
+        result["stage2_b64_s32"] = stage2_time(dev, flush, timer, w, mid)
+        del caches
+        result["stage1_ragged_b64"] = stage1_workload_time(dev, flush, timer, workloads.ragged_b64())
+        result["stage1_gqa8_b8_ctx32768"] = stage1_workload_time(dev, flush, timer,
+                                                                 workloads.gqa8_b8_ctx32768())
+        result["stream_ceiling"] = stream_ceiling(dev, timer)
         result["store"] = store_times(dev, flush, timer)
         result["full_decode"] = full_decode_time(dev, flush, timer)
         # Stage1 of the other presets at the same B64 x 4096 shape (each in its own layout)
@@ -492,10 +590,14 @@ def main() -> int:
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = src.nbytes
     if not args.no_cpu_baseline:
+        # the host cores this process may use, capped by OMP_NUM_THREADS when it is set (a
+        # GPU's share of a shared host)
         try:
-            threads = min(16, len(os.sched_getaffinity(0)))
+            threads = len(os.sched_getaffinity(0))
         except AttributeError:
-            threads = min(16, os.cpu_count() or 1)
+            threads = os.cpu_count() or 1
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        threads = min(threads, cap) if cap > 0 else threads
         result["cpu_baseline"] = cpu_baseline(w, threads)
         result["cpu_baseline_c"] = cpu_baseline_c(w, threads)
     print(json.dumps(result))

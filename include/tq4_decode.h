@@ -13,7 +13,14 @@
  * Shapes (row-major, contiguous):
  *   q_rot       float32 [B, Hq, D]            (D == 128)
  *   kv_cache    uint8   [num_blocks, block_size, Hk, slot]  slot = 134 at D=128,
- *               physical block stride = cache_block_stride bytes
+ *               physical block stride = cache_block_stride bytes.  Inside a block, SoA
+ *               has its own layout; an AoS slot (t, h) starts at (t*Hk + h)*slot
+ *               (TQ4_LAYOUT_AOS, position-major) or at (h*block_size + t)*slot
+ *               (TQ4_LAYOUT_AOS_HEAD_MAJOR: the vLLM backend's [blocks, Hk, block_size,
+ *               slot] cache, which it passes as kv_cache.transpose(1, 2),
+ *               reference/turboquant_attn.py:536, :565; the reference AoS kernels take
+ *               that view's stride(1) / stride(2), reference/aos_decode.py:563-565,
+ *               reference/aos_store.py:375-377)
  *   block_table int32   [B, max_blocks_per_seq]
  *   seq_lens    int32   [B]
  *   pair_lut    float32 [256, 2]              row lo*16+hi = (c[lo], c[hi])
@@ -31,12 +38,12 @@ extern "C" {
 
 typedef struct ihipStream_t *tq4_stream_t; /* same type as hipStream_t */
 
-enum tq4_layout { TQ4_LAYOUT_SOA = 0, TQ4_LAYOUT_AOS = 1 };
+enum tq4_layout { TQ4_LAYOUT_SOA = 0, TQ4_LAYOUT_AOS = 1, TQ4_LAYOUT_AOS_HEAD_MAJOR = 2 };
 enum tq4_dtype { TQ4_F32 = 0, TQ4_BF16 = 1, TQ4_F16 = 2 };
 enum tq4_kernel {
     TQ4_KERNEL_AUTO = 0,
     TQ4_KERNEL_SIMPLE = 1,
-    TQ4_KERNEL_MFMA = 2,
+    TQ4_KERNEL_MFMA = 2,   /* retired 4x4x4 MFMA kernel: rejected with TQ4_E_UNSUPPORTED */
     TQ4_KERNEL_XDL = 3
 };
 enum tq4_status {
@@ -65,12 +72,11 @@ int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block
                tq4_stream_t stream);
 
 /* Same as tq4_stage1 with an explicit kernel choice (TQ4_KERNEL_*): SIMPLE is the
- * plain-VALU kernel (any GQA group up to 16); MFMA (v_mfma_f32_4x4x4_16b_f16) and XDL
- * (v_mfma_f32_16x16x32_f16) are the matrix-core kernels (GQA group 4 or 8, block_size a
- * power of two >= 16, cache_block_stride a multiple of 16).  AUTO picks XDL when it
- * applies, SIMPLE otherwise.  sinks (fp32 [Hq], may be NULL): per-head sink logits in the
- * score domain (q.k * attn_scale); split 0 starts its softmax with max = sink, sum = 1
- * (XDL and SIMPLE kernels; MFMA rejects them).
+ * plain-VALU kernel (any GQA group up to 16); XDL (v_mfma_f32_16x16x32_f16) is the
+ * matrix-core kernel (GQA group 4 or 8, block_size a power of two >= 16,
+ * cache_block_stride a multiple of 16).  AUTO picks XDL when it applies, SIMPLE
+ * otherwise.  sinks (fp32 [Hq], may be NULL): per-head sink logits in the score domain
+ * (q.k * attn_scale); split 0 starts its softmax with max = sink, sum = 1.
  * Replaces: the per-version entry points tq4_cuda_v1 .. tq4_cuda_v9 (cuda/tq4_cuda_vN_bind.cpp);
  *           the sinks of _tq_decode_stage1 reference/soa_decode_v1.py:134-148. */
 int tq4_stage1_ex(const float *q_rot, const uint8_t *kv_cache, const int32_t *block_table,
@@ -121,7 +127,8 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
  * norm, x_hat = k / (norm + 1e-8), y = x_hat @ rot_t (rot_t = PiT, [D, D] fp32), 4-bit
  * index = number of the 15 midpoints <= y, stored scalar fp16(norm / ||c[idx]||) when
  * norm_correction is nonzero (centroids [16] required), else fp16(norm).  V: 4-bit
- * uniform codes with fp16 scale and fp16 min.  layout TQ4_LAYOUT_SOA or TQ4_LAYOUT_AOS.
+ * uniform codes with fp16 scale and fp16 min.  layout TQ4_LAYOUT_SOA, TQ4_LAYOUT_AOS or
+ * TQ4_LAYOUT_AOS_HEAD_MAJOR.
  * Replaces: triton_turboquant_store reference/soa_store.py:381-524 (MSE path, 4-bit keys
  *           and values; kernel :223-380) and the AoS writer reference/aos_store.py.
  */
@@ -145,8 +152,7 @@ int tq4_stage1_fp8(const float *query, const uint8_t *kv_cache, const int32_t *b
                    int max_blocks_per_seq, int64_t cache_block_stride, int num_kv_splits, int layout,
                    float attn_scale, const float *sinks, tq4_stream_t stream);
 
-/* tq4_stage1_fp8 with the kernel choice of tq4_stage1_ex (AUTO, SIMPLE or XDL; MFMA is
- * rejected).  Replaces: the same reference entry as tq4_stage1_fp8. */
+/* tq4_stage1_fp8 with the kernel choice of tq4_stage1_ex (AUTO, SIMPLE or XDL).  Replaces: the same reference entry as tq4_stage1_fp8. */
 int tq4_stage1_fp8_ex(const float *query, const uint8_t *kv_cache, const int32_t *block_table,
                       const int32_t *seq_lens, float *mid_o, int B, int Hq, int Hk, int D, int block_size,
                       int max_blocks_per_seq, int64_t cache_block_stride, int num_kv_splits, int layout,
@@ -154,7 +160,7 @@ int tq4_stage1_fp8_ex(const float *query, const uint8_t *kv_cache, const int32_t
 
 /*
  * FP8-key preset writer: K cast to E4M3 (round to nearest even, saturating at +-448, NaN
- * kept), V as tq4_store; layout TQ4_LAYOUT_SOA or TQ4_LAYOUT_AOS; slots < 0 skipped.
+ * kept), V as tq4_store; layout as tq4_store; slots < 0 skipped.
  * Replaces: _tq_fused_store_fp8 reference/soa_store.py:125-212 (launch :446-478) and the
  *           AoS FP8 store of reference/aos_store.py.
  */
@@ -209,7 +215,8 @@ int tq4_store_preset(const void *key, const void *value, int dtype, const int32_
  * Replaces: the TORCH_CHECK messages of cuda/tq4_cuda_v1.cu:468-499. */
 const char *tq4_last_error(void);
 
-/* ABI version of this library (major*100 + minor). */
+/* ABI version of this library (major*100 + minor): 106 adds TQ4_LAYOUT_AOS_HEAD_MAJOR and
+ * retires TQ4_KERNEL_MFMA. */
 int tq4_abi_version(void);
 
 /*

@@ -1,3 +1,6 @@
+# The Lloyd-Max iteration follows reference/centroids.py (SPDX-License-Identifier:
+# Apache-2.0, Copyright contributors to the vLLM project) step for step, so that the
+# centroids are bit-identical; the code is written anew.
 """Lloyd-Max codebook and pair LUT (oracle side).
 
 ``lloyd_max`` restates ``reference/centroids.py:18-79``: a Lloyd-Max scalar quantiser

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
                         text=True, check=True).stdout
     exported = set(re.findall(r" T (tq4_\w+)$", nm, re.M))
     assert set(declared()) <= exported
-    assert _lib.load().tq4_abi_version() == 105
+    assert _lib.load().tq4_abi_version() == 106
 
 
 def _stage1_call(**over):
@@ -77,3 +77,31 @@ def test_python_wrappers_mirror_reference_checks():
         ops.stage1(q, cache, bt, sl, lut, num_kv_splits=4)
     with pytest.raises(RuntimeError, match="centroids must be CUDA"):
         ops.launch_soa_v1_stage1(q, cache, bt, sl, torch.zeros(16), torch.zeros(2, 32, 4, 129))
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_cache_views_the_backend_passes(layout):
+    """The contiguous cache and the backend's ``transpose(1, 2)`` view of its head-major
+    ``[blocks, Hk, bs, slot]`` cache (reference/turboquant_attn.py:536, :565) are accepted; an
+    AoS view of the head-major cache selects the head-major slot strides."""
+    from tq4_decode.layout import AOS, AOS_HEAD_MAJOR, SOA
+
+    pm = torch.zeros(6, 16, 8, 134, dtype=torch.uint8)
+    hm = torch.zeros(6, 8, 16, 134, dtype=torch.uint8).transpose(1, 2)
+    geo = lambda t: ops.block_geometry(tuple(t.shape), t.stride(), 134, layout)  # noqa: E731
+    base = SOA if layout == "soa" else AOS
+    assert geo(pm) == (16, 8, 17152, base)
+    assert geo(hm) == (16, 8, 17152, SOA if layout == "soa" else AOS_HEAD_MAJOR)
+    # padded blocks keep their stride; one kv-head: both orders coincide
+    padded = torch.zeros(6, 17200, dtype=torch.uint8)[:, :17152].view(6, 16, 8, 134)
+    assert geo(padded)[2] == 17200
+    one = torch.zeros(6, 1, 16, 134, dtype=torch.uint8).transpose(1, 2)
+    assert ops.block_geometry(tuple(one.shape), one.stride(), 134, layout)[3] == base
+    bad = [torch.zeros(6, 16, 8, 268, dtype=torch.uint8)[..., ::2],          # strided slot bytes
+           torch.zeros(16, 6, 8, 134, dtype=torch.uint8).transpose(0, 1),   # blocks interleaved
+           torch.zeros(6, 16, 8, 140, dtype=torch.uint8)[..., :134]]        # padded slots
+    for t in bad:
+        with pytest.raises(RuntimeError, match="kv_cache"):
+            geo(t)
+    with pytest.raises(RuntimeError, match="slot_size=134"):
+        ops.block_geometry((6, 16, 8, 118), (15104, 944, 118, 1), 134, layout)

@@ -1,7 +1,7 @@
 """FP8-key preset (turboquant_k8v4) on the GPU: the writer bit-exact against the oracle
 writer (K bytes = E4M3 of the raw key, round to nearest even, saturating at +-448; V as
-the 4-bit writer), and Stage1 / the decode entry against the oracle (max-abs 1e-4 x
-max(1, max|ref|), fp32)."""
+the 4-bit writer), and Stage1 / the decode entry against the oracle (max-abs 1e-4,
+fp32)."""
 import numpy as np
 import pytest
 import torch
@@ -66,10 +66,7 @@ def _stage1(dev, w, cache, query, splits, layout, sinks=None, kernel="auto"):
 
 
 def _assert_parity(got, ref, tol=1e-4):
-    """Max-abs bound 1e-4 scaled by max(1, max|ref|): the MFMA kernel carries the softmax
-    weights as f16 hi + lo parts, ~4e-5 relative, and this cache's outputs reach ~3 (V ~
-    N(0, 1)); the 4-bit workloads' outputs stay below 1."""
-    tol = tol * max(1.0, float(np.nanmax(np.abs(ref))))
+    """Max-abs bound 1e-4 on every mid_o value (outputs and LSE, fp32)."""
     assert np.array_equal(np.isnan(got), np.isnan(ref)), "untouched-split pattern differs"
     err = np.nanmax(np.abs(got - ref))
     print(f"max-abs {err:.3e}")
@@ -103,7 +100,12 @@ def test_stage1_fp8_every_finite_byte(dev):
     ref = ostage.stage1(query, cache, w.block_table, w.seq_lens, None, 4, num_kv_heads=HK, key_fp8=True)
     for kernel in ("simple", "xdl"):
         got = _stage1(dev, w, cache, query, 4, "soa", kernel=kernel)
-        _assert_parity(got, ref, tol=1e-4 * max(1.0, float(np.nanmax(np.abs(ref)))))
+        # E4M3 keys up to +-448 give scores (and LSEs) in the thousands, where one fp32 ulp
+        # is above 1e-4: the outputs keep the absolute bound, the LSE column a relative one
+        _assert_parity(got[..., :D], ref[..., :D])
+        lse_err = np.nanmax(np.abs(got[..., D] - ref[..., D]) / np.maximum(1.0, np.abs(ref[..., D])))
+        print(f"LSE relative {lse_err:.3e}")
+        assert lse_err <= 1e-4
 
 
 @pytest.mark.parametrize("kernel", ["simple", "xdl"])

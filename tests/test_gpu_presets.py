@@ -232,7 +232,7 @@ def test_preset_store_then_decode_entry(dev, preset, layout):
     diff = np.abs(out.float().cpu().numpy()[live] - ro)
     print(f"{layout} {kb}/{vb} decode entry fp16 max-abs {diff.max():.3e}")
     # fp16 output: rounding to nearest (2^-11 relative) on top of the fp32 Stage1 bound
-    assert np.all(diff <= 2.0 ** -11 * np.abs(ro) + 1e-4 * max(1.0, float(np.abs(ro).max())))
+    assert np.all(diff <= 2.0 ** -11 * np.abs(ro) + 1e-4)
     with pytest.raises(RuntimeError):  # a cache of another slot size is rejected
         dec.triton_turboquant_decode_attention(
             t(query), cache, t(bt), t(lens), t(rot_t.T.copy()), t(cents), 1 / math.sqrt(D),
@@ -245,7 +245,7 @@ def test_preset_store_then_decode_entry(dev, preset, layout):
 def test_stage1_k3_on_the_mfma_kernel(dev, layout, group, vb):
     """3-bit K / 4- or 3-bit V on the 16x16x32 kernel (the auto choice for GQA 4 / 8): many
     splits per wave, a 4096-token sequence, empty and one-token sequences, sinks.  Bound
-    1e-4 x max(1, max|ref|): the MFMA kernel carries the softmax weights as f16 hi + lo parts."""
+    1e-4 absolute on every mid_o value."""
     hk = 8 // (group // 4)
     bt, lens, cache, cents, rng = _preset_cache(460 + group, [4096, 0, 1, 333, 2049], hk, 3, vb, layout)
     q = rng.standard_normal((len(lens), hk * group, D)).astype(np.float32)
@@ -254,7 +254,7 @@ def test_stage1_k3_on_the_mfma_kernel(dev, layout, group, vb):
         got = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, sinks=sk, kernel="xdl")
         ref = ostage.stage1(q, cache, bt, lens, cents, 32, num_kv_heads=hk, is_aos=layout == "aos",
                             bits=(3, vb), sinks=sk)
-        _assert_parity(got, ref, tol=1e-4 * max(1.0, float(np.nanmax(np.abs(ref)))))
+        _assert_parity(got, ref, tol=2e-5)  # inside the 1e-4 bar: fp32-grade on this data
     auto = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, kernel="auto")
     xdl = _stage1(dev, q, cache, bt, lens, cents, 32, 3, vb, layout, kernel="xdl")
     assert np.array_equal(auto, xdl, equal_nan=True), "auto runs the 16x16x32 kernel"
@@ -272,4 +272,4 @@ def test_stage1_k3_mfma_larger_blocks(dev, layout, bs, vb):
     got = _stage1(dev, q, cache, bt, lens, cents, 8, 3, vb, layout, kernel="xdl")
     ref = ostage.stage1(q, cache, bt, lens, cents, 8, num_kv_heads=hk, block_size=bs,
                         is_aos=layout == "aos", bits=(3, vb))
-    _assert_parity(got, ref, tol=1e-4 * max(1.0, float(np.nanmax(np.abs(ref)))))
+    _assert_parity(got, ref)

@@ -38,7 +38,7 @@ def assert_parity(got, ref, tol=TOL):
     assert err <= tol, f"max-abs {err} > {tol}"
 
 
-@pytest.mark.parametrize("kernel", ["simple", "mfma", "xdl"])
+@pytest.mark.parametrize("kernel", ["simple", "xdl"])
 @pytest.mark.parametrize("layout", ["soa", "aos"])
 def test_store_fixture_b2_ctx256(config1, dev, kernel, layout):
     f = config1
@@ -46,10 +46,12 @@ def test_store_fixture_b2_ctx256(config1, dev, kernel, layout):
                            f["seq_lens"], f["centroids"], int(f["num_kv_splits"]),
                            int(f["num_kv_heads"]))
     got = run(w, dev, kernel, layout)
-    assert_parity(got, f[f"mid_{layout}"])
+    # the matrix-core kernel holds fp32-grade accuracy on store-written data (f16 hi + lo
+    # parts, V codes at the top of the f16 significand): 5e-6, inside the 1e-4 bar
+    assert_parity(got, f[f"mid_{layout}"], 5e-6 if kernel == "xdl" else TOL)
 
 
-@pytest.mark.parametrize("kernel", ["simple", "mfma", "xdl"])
+@pytest.mark.parametrize("kernel", ["simple", "xdl"])
 @pytest.mark.parametrize("layout", ["soa", "aos"])
 def test_ragged_with_empty_and_partial_splits(dev, kernel, layout):
     w = workloads.small(101, 6, [1, 3, 17, 100, 257, 999], 32)
@@ -58,15 +60,14 @@ def test_ragged_with_empty_and_partial_splits(dev, kernel, layout):
 
 
 @pytest.mark.parametrize("kernel,group", [("simple", 1), ("simple", 2), ("simple", 4),
-                                          ("simple", 8), ("simple", 16), ("mfma", 4),
-                                          ("mfma", 8), ("xdl", 4), ("xdl", 8)])
+                                          ("simple", 8), ("simple", 16), ("xdl", 4), ("xdl", 8)])
 def test_gqa_groups(dev, kernel, group):
     hk = 4
     w = workloads.small(102, 3, [77, 300, 1024], 7, num_q_heads=hk * group, num_kv_heads=hk)
     assert_parity(run(w, dev, kernel), oracle(w))
 
 
-@pytest.mark.parametrize("kernel", ["simple", "mfma", "xdl"])
+@pytest.mark.parametrize("kernel", ["simple", "xdl"])
 @pytest.mark.parametrize("bs", [32, 64])
 def test_larger_kv_blocks(dev, kernel, bs):
     w = workloads.small(103, 3, [130, 511, 64], 5, block_size=bs)
@@ -75,7 +76,7 @@ def test_larger_kv_blocks(dev, kernel, bs):
         assert_parity(run(w, dev, kernel, layout, cache), oracle(w, layout, cache))
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "xdl"])
+@pytest.mark.parametrize("kernel", ["simple", "xdl"])
 @pytest.mark.parametrize("mb,lens", [(4, [1, 60, 33]), (12, [190, 7, 160]), (13, [200, 150, 9]),
                                      (252, [4032, 1000, 2500]), (256, [4096, 17, 3000]),
                                      (260, [4100, 4000, 1])])
@@ -97,7 +98,6 @@ def test_large_scores_rescale_path(dev):
     """q scaled x40: scores span tens of units, so the running max moves often."""
     w = workloads.small(104, 2, [640, 333], 3)
     w.q_rot = (w.q_rot * 40).astype(np.float32)
-    assert_parity(run(w, dev, "mfma"), oracle(w))
     assert_parity(run(w, dev, "xdl"), oracle(w))
     assert_parity(run(w, dev, "simple"), oracle(w))
 
@@ -123,15 +123,45 @@ def test_xdl_qwen3_4b_b64_ctx4096_full_size(qwen, dev, layout):
     assert_parity(run(w, dev, "xdl", layout, cache), oracle(w, layout, cache))
 
 
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_xdl_on_store_written_cache_full_size(dev, layout):
+    """B64 x ctx 4096 over a cache the GPU writer filled from N(0, 1) keys and values (V
+    scales ~0.4 and zero points ~-3, the realistic case for the f16 hi + lo softmax weights,
+    unlike the synthetic caches' 0.01-0.1 scales)."""
+    from tq4_decode import codebook
+
+    rng = np.random.default_rng(131)
+    B, ctx, nb = 64, 4096, 64 * 256
+    bt = rng.permutation(nb).astype(np.int32).reshape(B, ctx // 16)
+    pos = np.arange(ctx)
+    slots = (bt[:, pos // 16] * 16 + pos % 16).reshape(-1).astype(np.int32)
+    gen = torch.Generator(device=dev).manual_seed(132)
+    key = torch.randn(B * ctx, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    value = torch.randn(B * ctx, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    cents = codebook.centroids(128, 4)
+    mids = ((cents[:-1] + cents[1:]) * np.float32(0.5)).astype(np.float32)
+    rot = workloads.random_orthogonal(rng, 128)
+    cache = torch.zeros(nb, 16, 8, 134, dtype=torch.uint8, device=dev)
+    ops.store(key, value, cache, to_dev(slots, dev), to_dev(rot, dev), to_dev(mids, dev),
+              to_dev(cents, dev), layout=layout, norm_correction=layout == "soa")
+    del key, value
+    q_rot = rng.standard_normal((B, 32, 128)).astype(np.float32)
+    w = workloads.Workload("store_written", q_rot, cache.cpu().numpy(), bt, np.full(B, ctx, np.int32),
+                           cents, 32, 8)
+    got = run(w, dev, "xdl", layout)
+    ref = oracle(w, layout)
+    assert_parity(got, ref, 1e-5)
+
+
 def test_xdl_ragged_and_gqa8_full_size(dev):
     for w in (workloads.ragged_b64(), workloads.gqa8_b8_ctx32768()):
         assert_parity(run(w, dev, "xdl"), oracle(w))
 
 
-def test_mfma_and_simple_agree_full_size(qwen, dev):
+def test_xdl_and_simple_agree_full_size(qwen, dev):
     w, _ = qwen
-    a, b = run(w, dev, "mfma"), run(w, dev, "simple")
-    assert_parity(a, b, 2e-5)
+    a, b = run(w, dev, "xdl"), run(w, dev, "simple")
+    assert_parity(a, b, 1e-5)
 
 
 def test_ragged_b64_full_size(dev):
@@ -191,9 +221,19 @@ def native_free_oracle(w, cache, layout, sinks):
                          num_kv_heads=w.num_kv_heads, is_aos=layout == "aos", sinks=sinks)
 
 
-def test_sinks_rejected_by_the_4x4x4_kernel(dev):
+def test_retired_kernel_id_is_rejected(dev):
+    """TQ4_KERNEL_MFMA (2), the retired 4x4x4 kernel, returns TQ4_E_UNSUPPORTED and leaves
+    mid_o untouched."""
+    from tq4_decode import _lib
+
     w = workloads.small(108, 1, [64], 2)
     t = lambda a: to_dev(a, dev)  # noqa: E731
-    with pytest.raises(RuntimeError):
-        ops.stage1(t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens), t(w.pair_lut),
-                   num_kv_splits=2, kernel="mfma", sinks=torch.zeros(32, device=dev))
+    q, c, bt, sl, lut = t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens), t(w.pair_lut)
+    mid = torch.full((1, 32, 2, 129), float("nan"), device=dev)
+    lib = _lib.load()
+    rc = lib.tq4_stage1_ex(q.data_ptr(), c.data_ptr(), bt.data_ptr(), sl.data_ptr(), lut.data_ptr(),
+                           mid.data_ptr(), 1, 32, 8, 128, 16, bt.size(1), c.stride(0), 2, 0,
+                           128 ** -0.5, 2, None, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 2 and b"retired" in lib.tq4_last_error()
+    assert torch.isnan(mid).all()

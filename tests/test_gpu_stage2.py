@@ -72,6 +72,32 @@ def test_rotate_query_matches_fp64(dev, dtype, rows):
     assert err <= 2e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_rotate_query_rows_of_any_magnitude(dev, dtype):
+    """Rows whose magnitudes lie far outside the f16 range (bf16 / fp32 up to 1e30, down to
+    1e-30) and rows mixing large and small elements: each row is scaled by a power of two
+    before the f16 split, so the error relative to the row's norm stays at the fp32 level."""
+    rng = np.random.default_rng(208)
+    rows = 96
+    x = rng.standard_normal((rows, 128))
+    mags = {torch.bfloat16: [1e30, 1e12, 7e4, 1.0, 1e-6, 1e-20, 1e-30],
+            torch.float32: [1e30, 1e12, 7e4, 1.0, 1e-6, 1e-20, 1e-30],
+            torch.float16: [1e4, 1.0, 1e-3, 1e-5]}[dtype]
+    x *= np.array(mags)[np.arange(rows) % len(mags)][:, None]
+    x[rows - 1, :64] *= 1e-3  # a row with a 1000x spread
+    x[rows - 2] = 0.0
+    q = torch.from_numpy(x.astype(np.float32)).to(dtype)
+    rot = workloads.random_orthogonal(rng, 128)
+    got = ops.rotate_query(q.to(dev), to_dev(rot, dev)).cpu().numpy().astype(np.float64)
+    ref = q.double().numpy() @ rot.astype(np.float64)
+    assert np.isfinite(got).all()
+    norm = np.maximum(np.linalg.norm(ref, axis=1, keepdims=True), 1e-300)
+    rel = (np.abs(got - ref) / norm).max()
+    print(f"{dtype} rotation error / row norm {rel:.3e}")
+    assert rel <= 2e-6
+    assert np.array_equal(got[rows - 2], np.zeros(128))
+
+
 def test_full_b256_ctx2048_bf16(dev):
     w = workloads.full_b256_ctx2048()
     t = lambda a: to_dev(a, dev)  # noqa: E731

@@ -225,3 +225,56 @@ def test_reference_module_names(dev):
             gv = gather(a.cpu().numpy(), slots[keep] // BS, slots[keep] % BS, h, BS, HK, D)[2]
             rv = gather(ref, slots[keep] // BS, slots[keep] % BS, h, BS, HK, D)[2]
             assert np.array_equal(gv, rv)
+
+
+def _hadamard(d):
+    h = np.ones((1, 1))
+    while h.shape[0] < d:
+        h = np.block([[h, h], [h, -h]])
+    return (h / np.sqrt(d)).astype(np.float32)
+
+
+@pytest.mark.parametrize("rotation", ["hadamard", "orthogonal"])
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_store_then_decode_against_unquantized_attention(dev, layout, rotation):
+    """The reference's store -> decode check (validation/store_decode.py:90-230): B64 x ctx
+    4096, N(0, 1) fp16 keys, values and queries, the Sylvester-Hadamard rotation
+    (:45-51) as PiT for both the writer and the query, the writer's cache decoded by the full
+    step (rotation, Stage1 over 32 splits, Stage2), and sequence 0 compared with attention
+    computed in float64 from the unquantized K / V (:54-67).  The reference publishes the 4-bit
+    quantization error of that comparison, output max / mean 0.0187 / 0.0028 and LSE 0.0065 /
+    0.0025 (README.md:254-257); the bounds here are twice those, which a norm folded the wrong
+    way exceeds.  A seeded random orthogonal rotation as well: it is not symmetric, so the
+    writer and the query rotation must agree on its orientation."""
+    B, ctx, S, HQ = 64, 4096, 32, 32
+    rot = _hadamard(D) if rotation == "hadamard" else workloads.random_orthogonal(np.random.default_rng(9), D)
+    cents = codebook.centroids(D, 4)
+    mids = ((cents[:-1] + cents[1:]) * np.float32(0.5)).astype(np.float32)
+    gen = torch.Generator(device=dev).manual_seed(20260814)
+    key = torch.randn(B * ctx, HK, D, generator=gen, device=dev, dtype=torch.float32).half()
+    value = torch.randn(B * ctx, HK, D, generator=gen, device=dev, dtype=torch.float32).half()
+    query = torch.randn(B, HQ, D, generator=gen, device=dev, dtype=torch.float32).half()
+    cache = torch.zeros(B * ctx // BS, BS, HK, 134, dtype=torch.uint8, device=dev)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    ops.store(key, value, cache, torch.arange(B * ctx, dtype=torch.int32, device=dev), t(rot), t(mids),
+              t(cents), layout=layout, norm_correction=layout == "soa")
+    bt = torch.arange(B * ctx // BS, dtype=torch.int32, device=dev).reshape(B, ctx // BS)
+    sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    out, lse = ops.full_decode(query, t(rot), cache, bt, sl, t(cents), S, layout=layout,
+                               out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    q0 = query[0].double().cpu().numpy()
+    k0 = key[:ctx].double().cpu().numpy()[:, np.arange(HQ) // (HQ // HK)]  # [t, h, d]
+    v0 = value[:ctx].double().cpu().numpy()[:, np.arange(HQ) // (HQ // HK)]
+    s = np.einsum("hd,thd->ht", q0, k0) / np.sqrt(D)
+    m = s.max(axis=1, keepdims=True)
+    p = np.exp(s - m)
+    ref_lse = (m[:, 0] + np.log(p.sum(axis=1)))
+    ref_out = np.einsum("ht,thd->hd", p / p.sum(axis=1, keepdims=True), v0)
+    eo = np.abs(out[0].cpu().numpy() - ref_out)
+    el = np.abs(lse[0].cpu().numpy() - ref_lse)
+    print(f"{layout} {rotation} quantization error vs fp32 attention: output max/mean {eo.max():.4g} / {eo.mean():.4g}, "
+          f"LSE max/mean {el.max():.4g} / {el.mean():.4g}")
+    assert np.isfinite(out.cpu().numpy()).all() and np.isfinite(lse.cpu().numpy()).all()
+    assert eo.max() <= 2 * 0.018739756 and eo.mean() <= 2 * 0.0028449418
+    assert el.max() <= 2 * 0.0064659119 and el.mean() <= 2 * 0.0024851561

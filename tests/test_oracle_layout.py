@@ -93,3 +93,60 @@ def test_value_quantisation_bounds():
     rec = codes * scale[..., None] + vmin[..., None]
     assert codes.min() == 0 and codes.max() == 15
     assert np.all(np.abs(rec - v) <= scale[..., None] * 0.5 + 1e-6)
+
+
+def test_norm_correction_keeps_the_key_norm():
+    """The _nc writers store fp16(||k|| / ||c[idx]||) (reference/soa_store.py:343-353), so the
+    decoded key folded * c[idx] has the raw key's norm, to the fp16 rounding of the scalar
+    (2^-11 relative).  Folding the other way (||k|| * ||c||) is off by ||c||^2 (~3-6 %)."""
+    rng = np.random.default_rng(6)
+    c = codebook.centroids(128, 4)
+    key = (rng.standard_normal((400, 4, 128)) * rng.uniform(0.1, 30, (400, 4, 1))).astype(np.float32)
+    rot = workloads.random_orthogonal(rng, 128)
+    idx, norm, folded = store.quantize_keys(key, rot, c)
+    cn = np.sqrt((c[idx].astype(np.float64) ** 2).sum(-1))
+    knorm = np.linalg.norm(key.astype(np.float64), axis=-1)
+    ratio = cn * folded.astype(np.float16).astype(np.float64) / knorm
+    assert np.abs(ratio - 1).max() <= 2.0 ** -11 + 1e-6
+    wrong = cn * cn * ratio  # the other fold direction
+    assert np.abs(wrong - 1).max() > 0.02
+
+
+def test_fixture_soa_and_aos_slots_hold_the_same_key():
+    """The config-1 fixture's two caches come from the same keys: equal K codes, and the SoA
+    folded norm times ||c[idx]|| equals the AoS raw norm within the two fp16 roundings."""
+    f = np.load(layout.__file__.replace("oracle/layout.py", "tests/golden/config1_b2_ctx256.npz"))
+    soa, aos, c = f["cache_soa"], f["cache_aos"], f["centroids"]
+    nb, bs, hk = soa.shape[:3]
+    data = soa.reshape(nb, -1)[:, :bs * hk * 128].reshape(nb, bs, hk, 128)
+    assert np.array_equal(data[..., :64], aos[..., :64])       # K codes
+    assert np.array_equal(data[..., 64:], aos[..., 66:130])    # V codes
+    meta = soa.reshape(nb, -1)[:, bs * hk * 128:].copy().view(np.float16).reshape(nb, hk, 3, bs)
+    folded = meta[:, :, 0, :].transpose(0, 2, 1).astype(np.float64)       # [nb, bs, hk]
+    raw = aos[..., 64:66].copy().view(np.float16)[..., 0].astype(np.float64)
+    kb = aos[..., :64]
+    cn = np.sqrt((c[kb & 15].astype(np.float64) ** 2 + c[kb >> 4].astype(np.float64) ** 2).sum(-1))
+    assert np.abs(folded * cn / raw - 1).max() <= 2 * 2.0 ** -11 + 1e-6
+    # V scale and zero are stored identically
+    assert np.array_equal(meta[:, :, 1, :].transpose(0, 2, 1), aos[..., 130:132].copy().view(np.float16)[..., 0])
+    assert np.array_equal(meta[:, :, 2, :].transpose(0, 2, 1), aos[..., 132:134].copy().view(np.float16)[..., 0])
+
+
+def test_soa_and_converted_aos_decode_alike():
+    """The reference's layout check at its benchmark shape (README.md:146, AoS V1 vs SoA V1
+    output max-abs 1.28e-5): the AoS cache converted from the B64 x ctx 4096 SoA cache (raw
+    norm = fp16(folded * ||c||), baseline/common.py:651-671) decodes (raw / ||c||) to the SoA
+    outputs within 2e-5, the LSE within the fp16 rounding of the norm; a decoder that folded
+    the norm the other way would differ by percents.  C oracle (fp32)."""
+    from oracle import native
+
+    w = workloads.qwen3_4b_b64_ctx4096()
+    aos = workloads.soa_to_aos(w.kv_cache, w.centroids, 8)
+    a = native.stage1(w.q_rot, w.kv_cache, w.block_table, w.seq_lens, w.centroids, 32, num_kv_heads=8)
+    b = native.stage1(w.q_rot, aos, w.block_table, w.seq_lens, w.centroids, 32, num_kv_heads=8,
+                      is_aos=True)
+    err = np.abs(a[..., :128] - b[..., :128]).max()  # the output columns, as README.md:146
+    lse = np.abs(a[..., 128] - b[..., 128]).max()
+    print(f"SoA vs converted AoS output max-abs {err:.3e}, LSE {lse:.3e}")
+    assert err <= 2e-5
+    assert lse <= 2.0 ** -10 * np.abs(a[..., 128]).max()  # fp16 rounding of the norm

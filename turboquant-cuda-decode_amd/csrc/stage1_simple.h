@@ -10,7 +10,8 @@
 // is exact in fp32).
 //
 // Covers any GQA group G <= 16 and any block size; it is the general fallback of
-// the MFMA kernel and its cross-check on the GPU.
+// the MFMA kernel and its cross-check on the GPU.  AoS slot (t, h) of a block starts at
+// t * slot_pos + h * slot_head (position-major or head-major blocks); SoA ignores both.
 #pragma once
 #include "tq4_device.h"
 
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
     const float *__restrict__ pair_lut, float *__restrict__ mid_o, const float *__restrict__ sinks,
     int num_q_heads, int num_kv_heads, int block_size, int max_blocks, int64_t block_stride,
-    int num_splits, float score_scale_log2) {
+    int slot_pos, int slot_head, int num_splits, float score_scale_log2) {
     const int sid = blockIdx.x;
     const int kvh = blockIdx.y;
     const int b = blockIdx.z;
@@ -122,8 +123,7 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
                 vscale = load_half(meta + 2 * block_size);
                 vzero = load_half(meta + 4 * block_size);
             } else {
-                constexpr int raw = kKBytes + 2 + kVBytes + 4, slot = raw + raw % 2;
-                kp = cache + blk * block_stride + ((int64_t)off * num_kv_heads + kvh) * slot;
+                kp = cache + blk * block_stride + (int64_t)off * slot_pos + (int64_t)kvh * slot_head;
                 norm = load_half(kp + kKBytes);
                 vp = kp + kKBytes + 2;
                 vscale = load_half(vp + kVBytes);
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
                 vscale = load_half(meta);
                 vzero = load_half(meta + 2 * block_size);
             } else {
-                kp = cache + blk * block_stride + ((int64_t)off * num_kv_heads + kvh) * (rec + 4);
+                kp = cache + blk * block_stride + (int64_t)off * slot_pos + (int64_t)kvh * slot_head;
                 vscale = load_half(kp + rec);
                 vzero = load_half(kp + rec + 2);
             }
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kWave) void stage1_simple_kernel(
             vscale = load_half(soa_meta(cache, blk, block_stride, off, num_kv_heads, kvh, block_size, 1));
             vzero = load_half(soa_meta(cache, blk, block_stride, off, num_kv_heads, kvh, block_size, 2));
         } else {
-            kp = aos_slot(cache, blk, block_stride, off, num_kv_heads, kvh);
+            kp = cache + blk * block_stride + (int64_t)off * slot_pos + (int64_t)kvh * slot_head;
             vp = kp + kHalfD + 2;
             norm = load_half(kp + kHalfD);
             vscale = load_half(kp + kHeadDim + 2);

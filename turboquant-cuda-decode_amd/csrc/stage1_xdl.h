@@ -29,8 +29,9 @@
 //   row rotations);  B[slot s][col n] = V code of the same token at dim 8n + j for MFMA
 //   j = 0..7, as an f16 bit pattern (lane (n, g) loads V dword n of tokens 4g .. 4g+3;
 //   v_perm_b32 packs two tokens' bytes).  Accumulator 2m takes the low nibbles (dim
-//   8n + 2m), accumulator 2m + 1 the whole bytes (dim 8n + 2m plus 16 x dim 8n + 2m + 1);
-//   D rows 4g + r hold part g >> 1 of the sums, in units of 2^-24.
+//   8n + 2m), accumulator 2m + 1 the whole bytes (dim 8n + 2m plus 16 x dim 8n + 2m + 1),
+//   both shifted to the top of the f16 significand (see pv_qk); D rows 4g + r hold part
+//   g >> 1 of the sums.
 //
 // Schedule: stage t = softmax of tile t, then QK^T of tile t + 1; odd stages also run
 // the PV of tiles (t-1, t), interleaved with that QK^T.  K loads run 4 tiles ahead of
@@ -86,12 +87,17 @@ __device__ __forceinline__ float rs_xor32(float a, float c) {
     return bitsf(r[0]) + bitsf(r[1]);
 }
 
-// f16 hi + lo parts of an fp32 value, packed (hi in bits 0..15, lo in 16..31), both
-// rounded toward zero: hi + lo = x to ~2^-20 relative.
+// f16 hi + lo parts of an fp32 value, packed (hi in bits 0..15, lo in 16..31): hi + lo =
+// x to 2^-22 relative while lo is a normal f16, else to half the f16 denormal step.  hi is
+// rounded toward zero (v_cvt_pkrtz, saturating), so lo has the sign of x: measured on
+// gfx950, the matrix core sums the eight products of a lane's k-slots with truncation
+// relative to the largest of them, and parts of one sign keep that error smallest (the PV
+// sums stay all-positive).  lo is rounded to nearest, so the residual error has no
+// preferred sign and does not build up over a split's tokens.  |x| must stay below 65504.
 __device__ __forceinline__ uint32_t split_f16(float x) {
     const auto h = __builtin_amdgcn_cvt_pkrtz(x, 0.f);
-    const float r = x - (float)h[0];
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, r));
+    const _Float16 l = (_Float16)(x - (float)h[0]);
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l) << 16);
 }
 __device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(half8, uint4{a, b, c, d});
@@ -173,34 +179,38 @@ template <int LAYOUT, bool KF8, bool KB3 = false> constexpr int v_offset() {
     return KF8 ? kHeadDim : (KB3 ? kK3Bytes : kHalfD) + (LAYOUT == 0 ? 0 : 2);
 }
 
+// Record (t, h) of a block starts at t * pos + h * head: SoA pos = Hk * rec, head = rec;
+// AoS position-major blocks [bs][Hk][slot] the same, head-major blocks [Hk][bs][slot] pos =
+// slot, head = bs * slot (the caller passes the AoS strides).
 template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false, bool V3 = false>
-__device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int hk, int block_size) {
+__device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int hk, int block_size, int pos,
+                                                    int head) {
     constexpr int TPL = G / 4;
     const int st = 4 * g + TPL * (n / G);  // first softmax token of the lane
     const int rec = record_bytes<LAYOUT, KF8, KB3, V3>();
+    if constexpr (LAYOUT == 0) {
+        pos = hk * rec;
+        head = rec;
+    }
     LaneOffsets o;
-    o.tok_stride = hk * rec;
+    o.tok_stride = pos;
     // K is loaded coalesced (each 16-lane row reads 4 whole 64-byte K records) and then
     // permuted across lanes into the MFMA layout (lane (n, g) = token n, bytes 16g ..).
-    o.k = ((4 * g + (n >> 2)) * hk + kvh) * rec + 16 * (n & 3);
-    if (KB3) {
-        // 3-bit keys: lane 16g + n loads 12 bytes, chunk (n & 3) of token 4g + (n >> 2), so
-        // four consecutive lanes read one whole 48-byte K record; lane (n, g) then takes
-        // chunk g of token n (the codes of dims 32g .. 32g+31) from lane 4n + g
-        o.k = ((4 * g + (n >> 2)) * hk + kvh) * rec + 12 * (n & 3);
-        o.kperm = 4 * (4 * n + g);
-    }
+    // KB3 (3-bit keys): lane 16g + n loads 12 bytes, chunk (n & 3) of token 4g + (n >> 2), so
+    // four consecutive lanes read one whole 48-byte K record; lane (n, g) then takes chunk g
+    // of token n (the codes of dims 32g .. 32g+31) from lane 4n + g, as in the 4-bit case.
+    o.k = (4 * g + (n >> 2)) * pos + kvh * head + (KB3 ? 12 : 16) * (n & 3);
     o.kperm = 4 * (16 * (n >> 2) + 4 * (n & 3) + g);
     // KF8: the second 64 K bytes are loaded the same way from o.k + 64
     // V3: the 3 bytes of dims 8n .. 8n+7 (a dword read; its fourth byte lies inside the
     // record or, for n = 15, is the next record's / the metadata's first byte, masked off)
-    o.v0 = (4 * g * hk + kvh) * rec + v_offset<LAYOUT, KF8, KB3>() + (V3 ? 3 : 4) * n;
+    o.v0 = 4 * g * pos + kvh * head + v_offset<LAYOUT, KF8, KB3>() + (V3 ? 3 : 4) * n;
     if (LAYOUT == 0) {
         // metadata fields: K norm, V scale, V zero (KF8: V scale, V zero)
         o.m = (kvh * (KF8 ? 2 : 3) * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
         o.mf = block_size * 2;
     } else {
-        o.m = (st * hk + kvh) * rec;
+        o.m = st * pos + kvh * head;
         o.mf = 0;
     }
     return o;
@@ -498,20 +508,28 @@ __device__ __forceinline__ floatx4 qk_tile(const KOps &k, const half8 (&bq)[8]) 
 }
 
 // PV of a pair of tiles (A operand aw, V dwords va / vb of tokens 4g .. 4g+3) interleaved
-// with QK^T of the next tile.  Accumulator 2m takes the even dim's codes (low nibbles),
-// accumulator 2m + 1 the whole bytes (lo + 16 * hi); the odd dim is recovered as
-// (acc[2m+1] - acc[2m]) / 16 when the split's rows are written.  V3 (3-bit values, dims
+// with QK^T of the next tile.  V codes enter as f16 denormal bit patterns (integer k <->
+// k * 2^-24), placed in the top bits of the 10-bit significand: the matrix core aligns a
+// product with a denormal factor at the denormal exponent, so every leading zero of the
+// significand would cut that product's share of the truncated in-lane sum.
+// Accumulator 2m takes the even dim's codes (low nibble << 6, units 2^-18), accumulator
+// 2m + 1 the whole bytes (byte << 2, units 2^-22: lo + 16 * hi); the odd dim is recovered as
+// (16 acc[2m+1] - acc[2m]) * 2^14 when the split's rows are written.  V3 (3-bit values, dims
 // 8n .. 8n+7 at bits 3(d - 8n) of the lane's dword): accumulator 2m takes the even dim's
-// codes, 2m + 1 the odd dim's, each a 3-bit field.
+// codes, 2m + 1 the odd dim's, each a 3-bit field << 7 (units 2^-17).
+constexpr float kVUnitEven = 262144.0f;  // 2^18: 4-bit low nibble << 6
+constexpr float kVUnitOdd = 16384.0f;    // 2^14: (16 * (byte << 2) - (nibble << 6)) units
+constexpr float kVUnit3 = 131072.0f;     // 2^17: 3-bit code << 7
 template <bool V3 = false>
 __device__ __forceinline__ floatx4 pv_qk(floatx4 (&acc)[8], const uint32_t (&aw)[4], const uint32_t (&va)[4],
                                          const uint32_t (&vb)[4], const KOps &k, const half8 (&bq)[8]) {
     const half8 a = as_half8(aw[0], aw[1], aw[2], aw[3]);
     floatx4 h = {0.f, 0.f, 0.f, 0.f}, l = {0.f, 0.f, 0.f, 0.f};
     if constexpr (V3) {
-        // codes of two tokens' dwords x, y at bit b -> (code_x, code_y) as u16 slots
+        // codes of two tokens' dwords x, y at bit b -> (code_x << 7, code_y << 7) as u16 slots
         auto pair = [](uint32_t x, uint32_t y, int b) {
-            return ((x >> b) & 7u) | (((y >> b) & 7u) << 16);
+            const uint32_t cx = b >= 7 ? (x >> (b - 7)) : (x << (7 - b));
+            return (cx & 0x380u) | ((y << (23 - b)) & 0x03800000u);
         };
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -532,10 +550,10 @@ __device__ __forceinline__ floatx4 pv_qk(floatx4 (&acc)[8], const uint32_t (&aw)
         const uint32_t p0 = __builtin_amdgcn_perm(va[1], va[0], sel), p1 = __builtin_amdgcn_perm(va[3], va[2], sel);
         const uint32_t p2 = __builtin_amdgcn_perm(vb[1], vb[0], sel), p3 = __builtin_amdgcn_perm(vb[3], vb[2], sel);
         h = mfma(k_operand(k, 2 * m), bq[2 * m], h);
-        acc[2 * m] = mfma(a, as_half8(p0 & 0x000F000Fu, p1 & 0x000F000Fu, p2 & 0x000F000Fu, p3 & 0x000F000Fu),
-                          acc[2 * m]);
+        acc[2 * m] = mfma(a, as_half8((p0 << 6) & 0x03C003C0u, (p1 << 6) & 0x03C003C0u, (p2 << 6) & 0x03C003C0u,
+                                      (p3 << 6) & 0x03C003C0u), acc[2 * m]);
         l = mfma(k_operand(k, 2 * m + 1), bq[2 * m + 1], l);
-        acc[2 * m + 1] = mfma(a, as_half8(p0, p1, p2, p3), acc[2 * m + 1]);
+        acc[2 * m + 1] = mfma(a, as_half8(p0 << 2, p1 << 2, p2 << 2, p3 << 2), acc[2 * m + 1]);
     }
     return h + l;
 }
@@ -596,15 +614,23 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
                                              const bool (&valid)[G / 4], uint32_t &p0, uint32_t &p1,
                                              uint32_t &d0, uint32_t &d1) {
     constexpr int TPL = G / 4;
-    float s2[TPL];
+    float s2[TPL], vscale[TPL], vzero[TPL];
     bool need = false;
 #pragma unroll
-    for (int j = 0; j < TPL; ++j)
+    for (int j = 0; j < TPL; ++j) {
         s2[j] = fmaf(dot[j], norm_f[j], st.negm);  // score - m
+        vscale[j] = half_at(t.scale, j);
+        vzero[j] = half_at(t.zero, j);
+    }
     if (__builtin_expect(boundary, 0)) {
+        // tokens outside the split: p = 0, and their (unwritten, possibly non-finite) V
+        // scale and zero must not reach p * scale, p * zero
 #pragma unroll
-        for (int j = 0; j < TPL; ++j)
+        for (int j = 0; j < TPL; ++j) {
             s2[j] = valid[j] ? s2[j] : -INFINITY;
+            vscale[j] = valid[j] ? vscale[j] : 0.f;
+            vzero[j] = valid[j] ? vzero[j] : 0.f;
+        }
     }
 #pragma unroll
     for (int j = 0; j < TPL; ++j)
@@ -663,8 +689,8 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
     for (int j = 0; j < TPL; ++j) {
         const float p = __builtin_amdgcn_exp2f(s2[j]);
         st.l += p;
-        st.z = fmaf(p, half_at(t.zero, j), st.z);
-        y[j] = split_f16(p * half_at(t.scale, j));
+        st.z = fmaf(p, vzero[j], st.z);
+        y[j] = split_f16(p * vscale[j]);
     }
     uint32_t P, Q;
     if constexpr (G == 4) {
@@ -715,18 +741,20 @@ __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc
     float oa[8], ob[8];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        // V codes entered as n * 2^-24; accumulator 2m + 1 holds (even + 16 * odd), or (V3)
-        // the odd dim's codes
+        // accumulator 2m + 1 holds the whole bytes (even + 16 * odd), or (V3) the odd dim's
+        // codes, in the units of pv_qk
         const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
         const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
-        oa[2 * m] = fmaf(xa, 16777216.0f, z_a) * inv_a;
-        ob[2 * m] = fmaf(xb, 16777216.0f, z_b) * inv_b;
         if constexpr (V3) {
-            oa[2 * m + 1] = fmaf(ya, 16777216.0f, z_a) * inv_a;
-            ob[2 * m + 1] = fmaf(yb, 16777216.0f, z_b) * inv_b;
+            oa[2 * m] = fmaf(xa, kVUnit3, z_a) * inv_a;
+            ob[2 * m] = fmaf(xb, kVUnit3, z_b) * inv_b;
+            oa[2 * m + 1] = fmaf(ya, kVUnit3, z_a) * inv_a;
+            ob[2 * m + 1] = fmaf(yb, kVUnit3, z_b) * inv_b;
         } else {
-            oa[2 * m + 1] = fmaf(ya - xa, 1048576.0f, z_a) * inv_a;
-            ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
+            oa[2 * m] = fmaf(xa, kVUnitEven, z_a) * inv_a;
+            ob[2 * m] = fmaf(xb, kVUnitEven, z_b) * inv_b;
+            oa[2 * m + 1] = fmaf(fmaf(ya, 16.f, -xa), kVUnitOdd, z_a) * inv_a;
+            ob[2 * m + 1] = fmaf(fmaf(yb, 16.f, -xb), kVUnitOdd, z_b) * inv_b;
         }
     }
     if (G == 8 || (lc.g & 1) == 0) {
@@ -770,10 +798,10 @@ __device__ __forceinline__ void emit_output(const State &st, const floatx4 (&acc
     for (int m = 0; m < 4; ++m) {
         const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
         const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
-        oa[2 * m] = fmaf(xa, 16777216.0f, z_a) * inv_a;
-        ob[2 * m] = fmaf(xb, 16777216.0f, z_b) * inv_b;
-        oa[2 * m + 1] = fmaf(ya - xa, 1048576.0f, z_a) * inv_a;
-        ob[2 * m + 1] = fmaf(yb - xb, 1048576.0f, z_b) * inv_b;
+        oa[2 * m] = fmaf(xa, kVUnitEven, z_a) * inv_a;
+        ob[2 * m] = fmaf(xb, kVUnitEven, z_b) * inv_b;
+        oa[2 * m + 1] = fmaf(fmaf(ya, 16.f, -xa), kVUnitOdd, z_a) * inv_a;
+        ob[2 * m + 1] = fmaf(fmaf(yb, 16.f, -xb), kVUnitOdd, z_b) * inv_b;
     }
     if (G == 8 || (lc.g & 1) == 0) {
         const int64_t ra = (row0 + hA) * kHeadDim + 8 * lc.n, rb = ra + kHeadDim;
@@ -834,7 +862,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const float *__restrict__ pair_lut, float *__restrict__ mid_o, const float *__restrict__ sinks,
     void *__restrict__ out, int out_dtype, float *__restrict__ lse,
     int num_q_heads, int num_kv_heads, int block_size_log2, int max_blocks, int64_t block_stride,
-    int num_splits, float score_scale_log2) {
+    int slot_pos, int slot_head, int num_splits, float score_scale_log2) {
     static_assert(G == 4 || G == 8, "GQA group 4 or 8");
     constexpr int TPL = G / 4;
     constexpr int RING = 4;
@@ -929,7 +957,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     total += tail;
     auto split_stop = [&](int s) { return ((split_tiles(s) + 1) & ~1) + (s == s_hi - 1 ? tail : 0); };
 
-    const LaneOffsets off = lane_offsets<LAYOUT, G, KF8, KB3, V3>(lc.n, lc.g, kvh, num_kv_heads, block_size);
+    const LaneOffsets off =
+        lane_offsets<LAYOUT, G, KF8, KB3, V3>(lc.n, lc.g, kvh, num_kv_heads, block_size, slot_pos, slot_head);
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
     const int tok0 = 4 * lc.g + TPL * (lc.n / G);  // the lane's first softmax token
     const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
@@ -1050,8 +1079,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         {
             const int blk = bt[(16 * tile_lane) >> block_size_log2];
             const int toff = (16 * tile_lane) & (block_size - 1);
+            // the piece's first record: token toff of kv-head 0 (AoS: at toff * slot_pos)
+            const int piece = LAYOUT == 0 ? toff * num_kv_heads * rec : toff * slot_pos;
             const uint64_t a = reinterpret_cast<uint64_t>(cache) + (uint64_t)((int64_t)blk * block_stride) +
-                               (uint64_t)(toff * num_kv_heads * rec);
+                               (uint64_t)piece;
             base_lo = (uint32_t)a;
             base_hi = (uint32_t)(a >> 32);
             moff_lane = (block_size - toff) * num_kv_heads * rec + toff * 2;

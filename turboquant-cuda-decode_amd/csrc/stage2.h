@@ -53,23 +53,42 @@ __global__ __launch_bounds__(kWave) void stage2_kernel(const float *__restrict__
 
 // Rotation on the f16 matrix cores: q_rot = query @ rot_t with rot_t split into f16
 // hi + lo parts (hi + lo = rot_t to ~2^-22), and for fp32 queries the query too
-// (products hi*hi + hi*lo + lo*hi; fp16 and bf16 queries are taken as f16, exact for the
-// magnitudes of attention queries).  A workgroup of 4 waves stages rot_t^T as f16 parts in
-// LDS (2 x 32 KB) and each wave rotates 16 rows: lane (n, g) feeds A[row n][k 8g .. 8g+7]
-// and B[k 8g .. 8g+7][col n] of v_mfma_f32_16x16x32_f16 and gets D[rows 4g .. 4g+3][col n].
+// (products hi*hi + hi*lo + lo*hi).  Each query row is first scaled by a power of two 2^e
+// that puts its largest magnitude in [2^14, 2^15) -- inside the f16 range for any fp32 or
+// bf16 row, and with the lo parts of the row's large elements out of f16 denormals -- and
+// the result row is scaled back by 2^-e (both exact).  fp16 and bf16 rows are then exact in
+// f16 (lo part 0) but for elements 2^29 times below the row's largest.  A workgroup of 4
+// waves stages rot_t^T as f16 parts in LDS (2 x 32 KB) and each wave rotates 16 rows: lane
+// (n, g) feeds A[row n][k 8g .. 8g+7] and B[k 8g .. 8g+7][col n] of
+// v_mfma_f32_16x16x32_f16 and gets D[rows 4g .. 4g+3][col n].
 constexpr int kRotWaves = 4;
 constexpr int kRotMfmaRows = 16 * kRotWaves;  // rows per workgroup
 constexpr int kRotPt = kHeadDim + 8;           // LDS row of rot_t^T (halves), 16-byte aligned
 typedef _Float16 rot_half8 __attribute__((ext_vector_type(8)));
 
 template <typename InT, typename V8>
-__device__ __forceinline__ void rot_a_operands(const V8 &p, rot_half8 &hi, rot_half8 &lo) {
+__device__ __forceinline__ void rot_a_operands(const V8 &p, int e, rot_half8 &hi, rot_half8 &lo) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const float x = to_float<InT>(p[j]);
+        const float x = __builtin_ldexpf(to_float<InT>(p[j]), e);
         hi[j] = (_Float16)x;
         lo[j] = sizeof(InT) == 4 ? (_Float16)(x - (float)hi[j]) : (_Float16)0.f;
     }
+}
+
+// Largest |x| of a query row over its four lanes n, n + 16, n + 32, n + 48.
+// (The swap results are read by value before the bit cast: a bit cast of the returned
+// vector's element lvalue reads its first element.)
+__device__ __forceinline__ float rot_row_max(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    uint32_t a = r[0], b = r[1];
+    x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    const uint32_t v = __builtin_bit_cast(uint32_t, x);
+    r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
 template <typename InT>
@@ -133,10 +152,24 @@ __global__ __launch_bounds__(kWave *kRotWaves) void rotate_mfma_kernel(const InT
     }
     if (r0 >= rows)
         return;
+    // the row's scale 2^e: max |x| * 2^e in [2^14, 2^15) (e = 0 for a zero or non-finite max)
+    float amax = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            amax = fmaxf(amax, fabsf(to_float<InT>(qv[kb][j])));
+    amax = rot_row_max(amax);
+    const int e = (amax > 0.f && amax < __builtin_inff()) ? 15 - __builtin_amdgcn_frexp_expf(amax) : 0;
+    // D row 4g + i is query row r0 + 4g + i, whose scale lane 4g + i (row n = 4g + i) holds
+    int e_out[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        e_out[i] = __shfl(e, 4 * g + i, kWave);
     rot_half8 a_hi[4], a_lo[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-        rot_a_operands<InT>(qv[kb], a_hi[kb], a_lo[kb]);
+        rot_a_operands<InT>(qv[kb], e, a_hi[kb], a_lo[kb]);
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -154,7 +187,7 @@ __global__ __launch_bounds__(kWave *kRotWaves) void rotate_mfma_kernel(const InT
         for (int i = 0; i < 4; ++i) {
             const int r = r0 + 4 * g + i;
             if (r < rows)
-                q_rot[(int64_t)r * kHeadDim + 16 * cb + n] = acc[i];
+                q_rot[(int64_t)r * kHeadDim + 16 * cb + n] = __builtin_ldexpf(acc[i], -e_out[i]);
         }
     }
 }

@@ -12,7 +12,9 @@
 //      0, 15), fp16 scale and fp16 min.
 // SoA: codes in the block's data region (record (t, h) = 64 K bytes then 64 V bytes),
 // the three fp16 scalars in its metadata region [h][field][t].  AoS (reference/aos_store.py):
-// 134-byte slot (t, h) = K bytes | fp16 norm | V bytes | fp16 scale | fp16 min.
+// 134-byte slot (t, h) = K bytes | fp16 norm | V bytes | fp16 scale | fp16 min, at byte
+// t * slot_pos + h * slot_head of its block (position-major or head-major blocks; the
+// reference's stride_cache_pos / stride_cache_head, reference/aos_store.py:375-377).
 //
 // A workgroup of 8 waves stages 16 * PiT^T in LDS as f16 hi + lo parts once, then its
 // waves walk the rows 16 at a time (grid-stride); the first tile's K and V loads are issued
@@ -189,7 +191,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
     const T *__restrict__ key, const T *__restrict__ value, const int32_t *__restrict__ slot_mapping,
     const float *__restrict__ pit, const float *__restrict__ midpoints, const float *__restrict__ centroids,
     uint8_t *__restrict__ cache, int rows, int num_kv_heads, int block_size, int64_t block_stride,
-    int norm_correction) {
+    int slot_pos, int slot_head, int norm_correction) {
     __shared__ __align__(16) _Float16 pt_hi[kHeadDim * kHeadDim];
     __shared__ __align__(16) _Float16 pt_lo[kHeadDim * kHeadDim];
     constexpr int kMids = (1 << KB) - 1;  // Lloyd-Max midpoints
@@ -374,8 +376,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
                         meta[2 * block_size] = half_bits(vmin);
                     }
                 } else {
-                    constexpr int raw = kK + 2 + kV + 4, slot_bytes = raw + raw % 2;
-                    uint8_t *sl = base + (off * num_kv_heads + head) * slot_bytes;
+                    uint8_t *sl = base + off * slot_pos + (int64_t)head * slot_head;
                     store_words_a2(sl + 4 * KB * g, kw);
                     store_words_a2(sl + kK + 2 + 4 * VB * g, vw);
                     if (g == 0) {
@@ -402,7 +403,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
                     meta[2 * block_size] = half_bits(vmin);
                 }
             } else {
-                uint8_t *sl = base + (off * num_kv_heads + head) * kAosSlot;
+                uint8_t *sl = base + off * slot_pos + (int64_t)head * slot_head;
                 store16_a2(sl + 16 * g, kb);
                 store16_a2(sl + kHalfD + 2 + 16 * g, vb);
                 if (g == 0) {
@@ -435,7 +436,8 @@ __global__ __launch_bounds__(kWave *kFp8Waves) void store_fp8_kernel(const T *__
                                                                      const int32_t *__restrict__ slot_mapping,
                                                                      uint8_t *__restrict__ cache, int rows,
                                                                      int num_kv_heads, int block_size,
-                                                                     int64_t block_stride) {
+                                                                     int64_t block_stride, int slot_pos,
+                                                                     int slot_head) {
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int n = lane & 15, g = lane >> 4;
     const int tiles = (rows + kRows - 1) / kRows;
@@ -465,8 +467,8 @@ __global__ __launch_bounds__(kWave *kFp8Waves) void store_fp8_kernel(const T *__
             continue;
         const int64_t blk = slot / block_size, off = slot % block_size;
         uint8_t *base = cache + blk * block_stride;
-        const int rec = LAYOUT == 0 ? kFp8Record : kFp8Record + 4;
-        uint32_t *r = reinterpret_cast<uint32_t *>(base + (off * num_kv_heads + head) * rec);
+        uint32_t *r = reinterpret_cast<uint32_t *>(
+            base + (LAYOUT == 0 ? (off * num_kv_heads + head) * kFp8Record : off * slot_pos + (int64_t)head * slot_head));
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             r[8 * g + i] = kw[i];

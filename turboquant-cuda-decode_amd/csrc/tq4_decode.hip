@@ -6,14 +6,13 @@
 // message instead of throwing.
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
-#include <cstdlib>
-
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "../../include/tq4_decode.h"
-#include "stage1_mfma.h"
 #include "stage1_simple.h"
 #include "stage1_xdl.h"
 #include "stage2.h"
@@ -79,7 +78,7 @@ struct Stage1Args {
     float *mid_o;
     int B, Hq, Hk, D, bs, max_blocks;
     int64_t stride;
-    int S, layout;
+    int S, layout;  // TQ4_LAYOUT_*
     float scale;
     const float *sinks = nullptr;  // [Hq] sink logits of split 0, or null
     // set: one split per sequence, the XDL kernel writes the final rows (Stage2 fused)
@@ -90,7 +89,27 @@ struct Stage1Args {
     // > 0: the key_bits / value_bits preset on the VALU kernel; lut holds the 2^key_bits
     // centroids (not the pair LUT)
     int key_bits = 0, value_bits = 4;
+    // filled by check_stage1: kernel layout (0 SoA, 1 AoS) and the AoS slot strides
+    int kl = 0, slot_pos = 0, slot_head = 0;
 };
+
+// Kernel layout (0 SoA, 1 AoS) of an ABI layout id and the byte offsets of AoS slot (t, h)
+// inside a block, t * pos + h * head: position-major blocks [bs][Hk][slot] (TQ4_LAYOUT_AOS)
+// or head-major blocks [Hk][bs][slot] (TQ4_LAYOUT_AOS_HEAD_MAJOR, the layout the vLLM
+// backend's [blocks, Hk, bs, slot] cache presents through transpose(1, 2),
+// reference/turboquant_attn.py:536, :565).  SoA blocks are addressed by their own layout.
+struct CacheGeom {
+    int kl, pos, head;
+};
+bool layout_valid(int layout) {
+    return layout == TQ4_LAYOUT_SOA || layout == TQ4_LAYOUT_AOS || layout == TQ4_LAYOUT_AOS_HEAD_MAJOR;
+}
+CacheGeom cache_geom(int layout, int bs, int hk, int slot) {
+    if (layout == TQ4_LAYOUT_AOS_HEAD_MAJOR)
+        return {1, slot, bs * slot};
+    return {layout == TQ4_LAYOUT_AOS ? 1 : 0, hk * slot, slot};
+}
+#define TQ4_LAYOUT_MSG "layout must be 0 (SoA), 1 (AoS) or 2 (AoS, head-major blocks)"
 
 // Bytes of one AoS slot (= SoA bytes per (token, kv-head)) of a key_bits / value_bits preset.
 int preset_slot_bytes(int key_bits, int value_bits) {
@@ -104,7 +123,7 @@ bool preset_supported(int key_bits, int value_bits) {
 static_assert(tq4::kOutF32 == TQ4_F32 && tq4::kOutBf16 == TQ4_BF16 && tq4::kOutF16 == TQ4_F16,
               "output type ids");
 
-int check_stage1(const Stage1Args &a) {
+int check_stage1(Stage1Args &a) {
     if (!a.q_rot || !a.cache || !a.bt || !a.seq_lens || (!a.lut && !a.key_fp8) || !a.mid_o)
         return fail(TQ4_E_INVALID, "tq4_stage1: null pointer argument");
     if (a.B <= 0 || a.Hq <= 0 || a.Hk <= 0 || a.S <= 0 || a.bs <= 0 || a.max_blocks <= 0)
@@ -114,8 +133,8 @@ int check_stage1(const Stage1Args &a) {
         return fail(TQ4_E_INVALID, "tq4_stage1: Hq (%d) must be a multiple of Hk (%d)", a.Hq, a.Hk);
     if (a.D != tq4::kHeadDim)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: head_dim %d unsupported (kernels are built for 128)", a.D);
-    if (a.layout != TQ4_LAYOUT_SOA && a.layout != TQ4_LAYOUT_AOS)
-        return fail(TQ4_E_INVALID, "tq4_stage1: layout must be 0 (SoA) or 1 (AoS)");
+    if (!layout_valid(a.layout))
+        return fail(TQ4_E_INVALID, "tq4_stage1: " TQ4_LAYOUT_MSG);
     const int slot = a.key_fp8 ? tq4::store::kFp8Record + 4
                                : (a.key_bits > 0 ? preset_slot_bytes(a.key_bits, a.value_bits) : tq4::kAosSlot);
     const int64_t min_stride = (int64_t)a.bs * a.Hk * slot;
@@ -126,6 +145,10 @@ int check_stage1(const Stage1Args &a) {
         return fail(TQ4_E_INVALID, "tq4_stage1: kv_cache and q_rot must be 16-byte aligned");
     if (!(a.scale > 0.f) || a.scale != a.scale)
         return fail(TQ4_E_INVALID, "tq4_stage1: attn_scale must be positive");
+    const CacheGeom geom = cache_geom(a.layout, a.bs, a.Hk, slot);
+    a.kl = geom.kl;
+    a.slot_pos = geom.pos;
+    a.slot_head = geom.head;
     return TQ4_OK;
 }
 
@@ -142,55 +165,41 @@ template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t
         kernel = &tq4::stage1_simple_kernel<LAYOUT, G, false, 3, 3>;
     launch(kernel, grid, dim3(tq4::kWave), st,
                        a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.sinks, a.Hq, a.Hk, a.bs,
-                       a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
+                       a.max_blocks, a.stride, a.slot_pos, a.slot_head, a.S, a.scale * tq4::kLog2e);
 }
 
-// Waves per (sequence, kv-head) for the MFMA kernel; wave x takes splits
+// Waves per (sequence, kv-head) for the 16x16x32 kernel; wave x takes splits
 // [x * S / W, (x + 1) * S / W).  Consecutive splits in one wave share one load
 // pipeline, which removes per-split start-up latency; W is chosen so the grid fills
-// whole rounds of the waves the GPU holds at the kernel's occupancy.
-// TQ4_STAGE1_WAVES overrides W (a tuning knob; results do not depend on it).
-#ifndef TQ4_STAGE1_RING
-#define TQ4_STAGE1_RING 4
-#endif
-constexpr int kStage1Ring = TQ4_STAGE1_RING;  // tiles in flight per wave
-
-int waves_per_sequence(const Stage1Args &a, const void *kernel, int &slots) {
+// whole rounds of the waves the GPU holds at the kernel's occupancy.  `slots` caches that
+// count per kernel instance (computed on the first call; concurrent first calls compute the
+// same value).  TQ4_STAGE1_WAVES overrides W (a tuning knob; results do not depend on it).
+int waves_per_sequence(const Stage1Args &a, const void *kernel, std::atomic<int> &slots) {
     static const int forced = [] {
         const char *e = getenv("TQ4_STAGE1_WAVES");
         return e ? atoi(e) : 0;
     }();
     if (forced > 0)
         return forced < a.S ? forced : a.S;
-    if (!slots) {  // waves the device holds at once for this kernel
+    int held = slots.load(std::memory_order_relaxed);
+    if (!held) {  // waves the device holds at once for this kernel
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, tq4::kWave, 0) == hipSuccess &&
             cus > 0 && per_cu > 0)
-            slots = cus * per_cu;
+            held = cus * per_cu;
         else
-            slots = 256 * 4 * 2;
+            held = 256 * 4 * 2;
+        slots.store(held, std::memory_order_relaxed);
     }
     const int64_t pairs = (int64_t)a.Hk * a.B;
     // smallest number of whole rounds that gives every pair at least one wave
-    const int64_t rounds = (pairs + slots - 1) / slots;
-    int64_t w = rounds * slots / pairs;
+    const int64_t rounds = (pairs + held - 1) / held;
+    int64_t w = rounds * held / pairs;
     if (w < 1)
         w = 1;
     return (int)(w < a.S ? w : a.S);
-}
-
-template <int LAYOUT, int NSET> void launch_mfma(const Stage1Args &a, hipStream_t st) {
-    static int slots = 0;
-    const dim3 grid(a.Hk,
-                    waves_per_sequence(a, reinterpret_cast<const void *>(
-                                              &tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>),
-                                       slots),
-                    a.B);
-    launch(&tq4::stage1_mfma_kernel<LAYOUT, NSET, kStage1Ring>, grid, dim3(tq4::kWave), st,
-                       a.q_rot, a.cache, a.bt, a.seq_lens, a.lut, a.mid_o, a.Hq, a.Hk,
-                       log2_int(a.bs), a.max_blocks, a.stride, a.S, a.scale * tq4::kLog2e);
 }
 
 // Waves per SIMD the 16x16x32 kernel is built for.  Two: the SoA G=4 kernel also fits
@@ -203,7 +212,7 @@ template <int LAYOUT, int G> constexpr int xdl_waves_per_simd() {
 }
 
 template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false, bool V3 = false> int xdl_waves(const Stage1Args &a) {
-    static int slots = 0;
+    static std::atomic<int> slots{0};
     const auto kernel = &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, xdl_waves_per_simd<LAYOUT, G>(), false, KF8, KB3, V3>;
     return waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots);
 }
@@ -224,7 +233,7 @@ template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st
                     : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, false, true>;
     launch(kernel, grid, dim3(tq4::kWave), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
            a.mid_o, a.sinks, a.out, a.out_dtype, a.lse, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks,
-           a.stride, a.S, a.scale * tq4::kLog2e);
+           a.stride, a.slot_pos, a.slot_head, a.S, a.scale * tq4::kLog2e);
 }
 
 template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
@@ -247,17 +256,6 @@ bool mfma_applies(const Stage1Args &a) {
     return (g == 4 || g == 8) && pow2 && a.stride % 16 == 0;
 }
 
-template <int LAYOUT> int dispatch_mfma(const Stage1Args &a, hipStream_t st) {
-    if (!mfma_applies(a))
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: MFMA kernel needs GQA group 4 or 8, a "
-                                       "power-of-two block_size >= 16 and a 16-byte block stride");
-    if (a.Hq / a.Hk == 4)
-        launch_mfma<LAYOUT, 1>(a, st);
-    else
-        launch_mfma<LAYOUT, 2>(a, st);
-    return launch_status("stage1_mfma");
-}
-
 template <int LAYOUT> int dispatch_xdl(const Stage1Args &a, hipStream_t st) {
     if (!mfma_applies(a))
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: XDL kernel needs GQA group 4 or 8, a "
@@ -275,19 +273,19 @@ int auto_xdl_waves(const Stage1Args &a) {
     if (!mfma_applies(a))
         return 0;
     const bool g4 = a.Hq / a.Hk == 4;
-    if (a.layout == TQ4_LAYOUT_SOA)
+    if (a.kl == 0)
         return g4 ? xdl_waves<0, 4>(a) : xdl_waves<0, 8>(a);
     return g4 ? xdl_waves<1, 4>(a) : xdl_waves<1, 8>(a);
 }
 
-int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
+int run_stage1(Stage1Args a, int kernel, hipStream_t st) {
     int rc = check_stage1(a);
     if (rc)
         return rc;
-    // AUTO: the 16x16x32 kernel wherever the MFMA kernels apply (both layouts), else VALU.
-    // The FP8-key preset runs on the VALU kernel.
-    if (a.key_fp8 && kernel == TQ4_KERNEL_MFMA)
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: FP8 keys run on the 16x16x32 or the VALU kernel");
+    // AUTO: the 16x16x32 kernel wherever it applies (both layouts), else VALU.
+    if (kernel == TQ4_KERNEL_MFMA)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_ex: the 4x4x4 MFMA kernel is retired; "
+                                       "TQ4_KERNEL_XDL (16x16x32) covers the same shapes");
     if (a.key_fp8 && a.out)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_fp8: no fused Stage2 for FP8 keys");
     // the bit-width presets: 3-bit K (4- or 3-bit V) also on the 16x16x32 kernel, 4/4 VALU
@@ -301,14 +299,10 @@ int run_stage1(const Stage1Args &a, int kernel, hipStream_t st) {
     if (kernel == TQ4_KERNEL_AUTO)
         kernel = (a.key_bits > 0 && !preset_xdl) ? TQ4_KERNEL_SIMPLE
                                                  : (mfma_applies(a) ? TQ4_KERNEL_XDL : TQ4_KERNEL_SIMPLE);
-    if (kernel == TQ4_KERNEL_MFMA && a.sinks)
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1_ex: sinks need the XDL or the VALU kernel");
-    if (kernel == TQ4_KERNEL_MFMA)
-        return a.layout == TQ4_LAYOUT_SOA ? dispatch_mfma<0>(a, st) : dispatch_mfma<1>(a, st);
     if (kernel == TQ4_KERNEL_SIMPLE)
-        return a.layout == TQ4_LAYOUT_SOA ? dispatch_simple<0>(a, st) : dispatch_simple<1>(a, st);
+        return a.kl == 0 ? dispatch_simple<0>(a, st) : dispatch_simple<1>(a, st);
     if (kernel == TQ4_KERNEL_XDL)
-        return a.layout == TQ4_LAYOUT_SOA ? dispatch_xdl<0>(a, st) : dispatch_xdl<1>(a, st);
+        return a.kl == 0 ? dispatch_xdl<0>(a, st) : dispatch_xdl<1>(a, st);
     return fail(TQ4_E_INVALID, "tq4_stage1_ex: unknown kernel id %d", kernel);
 }
 
@@ -346,15 +340,16 @@ int rotate_query(const void *query, int query_dtype, const float *rot_t, float *
 template <int KB, int VB>
 int launch_store(const void *key, const void *value, int dtype, const int32_t *slot_mapping,
                  const float *rot_t, const float *midpoints, const float *centroids, uint8_t *kv_cache,
-                 int rows, int Hk, int block_size, int64_t cache_block_stride, int layout,
+                 int rows, int Hk, int block_size, int64_t cache_block_stride, const CacheGeom &geom,
                  int norm_correction, hipStream_t st, const char *what) {
     const int per_group = tq4::store::kRows * tq4::store::kWaves;
     const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, tq4::store::kMaxGroups));
 #define TQ4_STORE_LAUNCH(L, T)                                                                            \
     launch(&tq4::store::store_kernel<L, T, KB, VB>, grid, dim3(tq4::kWave * tq4::store::kWaves), st,      \
            static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, midpoints,      \
-           centroids, kv_cache, rows, Hk, block_size, cache_block_stride, norm_correction)
-    switch (dtype * 2 + layout) {
+           centroids, kv_cache, rows, Hk, block_size, cache_block_stride, geom.pos, geom.head,              \
+           norm_correction)
+    switch (dtype * 2 + geom.kl) {
     case TQ4_F32 * 2 + 0: TQ4_STORE_LAUNCH(0, float); break;
     case TQ4_F32 * 2 + 1: TQ4_STORE_LAUNCH(1, float); break;
     case TQ4_BF16 * 2 + 0: TQ4_STORE_LAUNCH(0, __bf16); break;
@@ -378,7 +373,7 @@ int tq4_time_next_launch(void *start_event, void *stop_event) {
     return ok();
 }
 
-int tq4_abi_version(void) { return 105; }
+int tq4_abi_version(void) { return 106; }
 
 const char *tq4_last_error(void) { return g_err; }
 
@@ -549,8 +544,8 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
         return fail(TQ4_E_INVALID, "tq4_store: N must be >= 0, Hk and block_size positive");
     if (D != tq4::kHeadDim)
         return fail(TQ4_E_UNSUPPORTED, "tq4_store: head_dim %d unsupported (128)", D);
-    if (layout != TQ4_LAYOUT_SOA && layout != TQ4_LAYOUT_AOS)
-        return fail(TQ4_E_INVALID, "tq4_store: layout must be 0 (SoA) or 1 (AoS)");
+    if (!layout_valid(layout))
+        return fail(TQ4_E_INVALID, "tq4_store: " TQ4_LAYOUT_MSG);
     const int64_t min_stride = (int64_t)block_size * Hk * tq4::kAosSlot;
     if (cache_block_stride < min_stride || cache_block_stride % 16)
         return fail(TQ4_E_INVALID, "tq4_store: requires cache [blocks,%d,%d,134]: block stride %lld",
@@ -563,7 +558,8 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
     if (N == 0)
         return ok();
     return launch_store<4, 4>(key, value, dtype, slot_mapping, rot_t, midpoints, centroids, kv_cache,
-                              N * Hk, Hk, block_size, cache_block_stride, layout, norm_correction,
+                              N * Hk, Hk, block_size, cache_block_stride,
+                              cache_geom(layout, block_size, Hk, tq4::kAosSlot), norm_correction,
                               reinterpret_cast<hipStream_t>(stream), "tq4_store");
 }
 
@@ -586,8 +582,8 @@ int tq4_store_preset(const void *key, const void *value, int dtype, const int32_
         return fail(TQ4_E_INVALID, "tq4_store_preset: N must be >= 0, Hk and block_size positive");
     if (D != tq4::kHeadDim)
         return fail(TQ4_E_UNSUPPORTED, "tq4_store_preset: head_dim %d unsupported (128)", D);
-    if (layout != TQ4_LAYOUT_SOA && layout != TQ4_LAYOUT_AOS)
-        return fail(TQ4_E_INVALID, "tq4_store_preset: layout must be 0 (SoA) or 1 (AoS)");
+    if (!layout_valid(layout))
+        return fail(TQ4_E_INVALID, "tq4_store_preset: " TQ4_LAYOUT_MSG);
     const int slot = preset_slot_bytes(key_bits, value_bits);
     const int64_t min_stride = (int64_t)block_size * Hk * slot;
     if (cache_block_stride < min_stride || cache_block_stride % 2)
@@ -601,12 +597,13 @@ int tq4_store_preset(const void *key, const void *value, int dtype, const int32_
     if (N == 0)
         return ok();
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const CacheGeom geom = cache_geom(layout, block_size, Hk, slot);
     if (value_bits == 4)
         return launch_store<3, 4>(key, value, dtype, slot_mapping, rot_t, midpoints, centroids, kv_cache,
-                                  N * Hk, Hk, block_size, cache_block_stride, layout, norm_correction, st,
+                                  N * Hk, Hk, block_size, cache_block_stride, geom, norm_correction, st,
                                   "tq4_store_preset");
     return launch_store<3, 3>(key, value, dtype, slot_mapping, rot_t, midpoints, centroids, kv_cache,
-                              N * Hk, Hk, block_size, cache_block_stride, layout, norm_correction, st,
+                              N * Hk, Hk, block_size, cache_block_stride, geom, norm_correction, st,
                               "tq4_store_preset");
 }
 
@@ -619,8 +616,8 @@ int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *
         return fail(TQ4_E_INVALID, "tq4_store_fp8: N must be >= 0, Hk and block_size positive");
     if (D != tq4::kHeadDim)
         return fail(TQ4_E_UNSUPPORTED, "tq4_store_fp8: head_dim %d unsupported (128)", D);
-    if (layout != TQ4_LAYOUT_SOA && layout != TQ4_LAYOUT_AOS)
-        return fail(TQ4_E_INVALID, "tq4_store_fp8: layout must be 0 (SoA) or 1 (AoS)");
+    if (!layout_valid(layout))
+        return fail(TQ4_E_INVALID, "tq4_store_fp8: " TQ4_LAYOUT_MSG);
     const int slot = tq4::store::kFp8Record + 4;
     const int64_t min_stride = (int64_t)block_size * Hk * slot;
     if (cache_block_stride < min_stride || cache_block_stride % 4)
@@ -637,11 +634,12 @@ int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *
     const int per_group = tq4::store::kRows * tq4::store::kFp8Waves;
     const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, 2048));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const CacheGeom geom = cache_geom(layout, block_size, Hk, slot);
 #define TQ4_STORE_FP8_LAUNCH(L, T)                                                                   \
     launch(&tq4::store::store_fp8_kernel<L, T>, grid, dim3(tq4::kWave * tq4::store::kFp8Waves), st, \
            static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, kv_cache, rows, Hk,  \
-           block_size, cache_block_stride)
-    switch (dtype * 2 + layout) {
+           block_size, cache_block_stride, geom.pos, geom.head)
+    switch (dtype * 2 + geom.kl) {
     case TQ4_F32 * 2 + 0: TQ4_STORE_FP8_LAUNCH(0, float); break;
     case TQ4_F32 * 2 + 1: TQ4_STORE_FP8_LAUNCH(1, float); break;
     case TQ4_BF16 * 2 + 0: TQ4_STORE_FP8_LAUNCH(0, __bf16); break;

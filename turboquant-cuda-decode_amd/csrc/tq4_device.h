@@ -71,10 +71,5 @@ __device__ __forceinline__ const uint8_t *soa_meta(const uint8_t *cache, int64_t
            (((int64_t)kvh * 3 + field) * block_size + off) * 2;
 }
 
-__device__ __forceinline__ const uint8_t *aos_slot(const uint8_t *cache, int64_t block,
-                                                   int64_t stride, int off, int num_kv_heads,
-                                                   int kvh) {
-    return cache + block * stride + ((int64_t)off * num_kv_heads + kvh) * kAosSlot;
-}
 
 }  // namespace tq4

@@ -1,3 +1,6 @@
+# The Lloyd-Max iteration follows reference/centroids.py (SPDX-License-Identifier:
+# Apache-2.0, Copyright contributors to the vLLM project) step for step, so that the
+# centroids are bit-identical; the code is written anew.
 """Lloyd-Max codebook for N(0, 1/d) and the byte-indexed pair LUT (host side).
 
 The codebook is the one the cache writer quantises K against: 2^bits centroids of

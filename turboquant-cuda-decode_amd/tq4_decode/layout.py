@@ -15,6 +15,11 @@ from __future__ import annotations
 
 SOA = 0
 AOS = 1
+# AoS with head-major blocks [Hk][bs][slot]: slot (t, h) at (h * bs + t) * slot.  The vLLM
+# backend allocates its cache [blocks, Hk, bs, slot] and hands the kernels
+# ``kv_cache.transpose(1, 2)`` (reference/turboquant_attn.py:536, :565); the host layer
+# picks this id from that view's strides.
+AOS_HEAD_MAJOR = 2
 LAYOUTS = {"soa": SOA, "aos": AOS}
 
 NUM_SOA_FIELDS = 3

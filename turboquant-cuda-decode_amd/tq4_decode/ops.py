@@ -27,9 +27,9 @@ import torch
 
 from . import _lib
 from ._lib import Tq4Error  # noqa: F401  (raised by every wrapper)
-from .layout import AOS, LAYOUTS, SOA, slot_bytes, slot_bytes_fp8, slot_bytes_preset
+from .layout import AOS, AOS_HEAD_MAJOR, LAYOUTS, SOA, slot_bytes, slot_bytes_fp8, slot_bytes_preset
 
-KERNELS = {"auto": 0, "simple": 1, "mfma": 2, "xdl": 3}
+KERNELS = {"auto": 0, "simple": 1, "xdl": 3}
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 HEAD_DIM = 128
 
@@ -55,6 +55,47 @@ def _layout_id(layout) -> int:
         return LAYOUTS[layout]
     _require(layout in (SOA, AOS), "layout must be 0 (SoA) or 1 (AoS)")
     return int(layout)
+
+
+def _cache_geometry(kv_cache: torch.Tensor, slot_want: int, layout, preset: str = ""):
+    """``(block_size, Hk, block stride, ABI layout id)`` of a cache tensor or view.
+
+    Takes the contiguous ``[blocks, block_size, Hk, slot]`` cache and the view the vLLM
+    backend passes, ``kv_cache.transpose(1, 2)`` of its ``[blocks, Hk, block_size, slot]``
+    allocation (``reference/turboquant_attn.py:536``, ``:565``).  SoA blocks are addressed
+    by their own layout, so only the block stride is read (as ``reference/soa_decode_v1.py:579``
+    and ``reference/soa_store.py:424`` do); AoS slots follow the view's position and head
+    strides (``reference/aos_decode.py:563-565``, ``reference/aos_store.py:375-377``), which
+    must describe a position-major or a head-major block.
+    """
+    _require(kv_cache.is_cuda, "kv_cache must be CUDA")
+    _require(kv_cache.dtype == torch.uint8, "kv_cache must be uint8")
+    _require(kv_cache.dim() == 4, "kv_cache must be [blocks, block_size, Hk, slot]")
+    return block_geometry(tuple(kv_cache.shape), kv_cache.stride(), slot_want, layout, preset)
+
+
+def block_geometry(shape, strides, slot_want: int, layout, preset: str = ""):
+    """The stride rules of ``_cache_geometry`` for a 4-D uint8 ``shape`` / ``strides``."""
+    nb, bs, hk, slot = shape
+    _require(slot == slot_want, f"requires slot_size={slot_want}{preset}")
+    s0, s1, s2, s3 = strides
+
+    def same(size, got, want):  # a dimension of size 1 has no meaningful stride
+        return size == 1 or got == want
+
+    _require(same(slot, s3, 1), "kv_cache: the slot bytes must be contiguous (stride(3) == 1)")
+    position_major = same(bs, s1, hk * slot) and same(hk, s2, slot)
+    head_major = same(bs, s1, slot) and same(hk, s2, bs * slot)
+    _require(position_major or head_major,
+             "kv_cache: each block must be a contiguous [block_size, Hk, slot] block or the "
+             "transpose(1, 2) view of a contiguous [Hk, block_size, slot] block")
+    block = bs * hk * slot
+    stride = s0 if nb > 1 else max(s0, block)
+    _require(stride >= block, "kv_cache: block stride is smaller than a block")
+    lid = _layout_id(layout)
+    if lid == AOS and not position_major:
+        lid = AOS_HEAD_MAJOR
+    return bs, hk, stride, lid
 
 
 def pair_lut_device(centroids: torch.Tensor) -> torch.Tensor:
@@ -83,16 +124,13 @@ def stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o=None, *, num_
     leave their ``mid_o`` rows untouched.  ``sinks`` (fp32 ``[Hq]``): per-head sink logits
     that split 0's softmax starts from (``reference/soa_decode_v1.py:134-148``).
     """
-    for t, n, dt in ((q_rot, "q_rot", torch.float32), (kv_cache, "kv_cache", torch.uint8),
-                     (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
-                     (pair_lut, "pair_lut", torch.float32)):
+    for t, n, dt in ((q_rot, "q_rot", torch.float32), (block_table, "block_table", torch.int32),
+                     (seq_lens, "seq_lens", torch.int32), (pair_lut, "pair_lut", torch.float32)):
         _check_tensor(t, n, dt)
     _require(q_rot.dim() == 3, "q_rot must be [B, Hq, D]")
     B, Hq, D = q_rot.shape
     _require(D == HEAD_DIM, f"requires D={HEAD_DIM}")
-    _require(kv_cache.dim() == 4, "kv_cache must be [blocks, block_size, Hk, slot]")
-    _, bs, Hk, slot = kv_cache.shape
-    _require(slot == slot_bytes(D), f"requires slot_size={slot_bytes(D)}")
+    bs, Hk, stride, lid = _cache_geometry(kv_cache, slot_bytes(D), layout)
     _require(Hq % Hk == 0, "Hq must be a multiple of Hk")
     _require(block_table.dim() == 2 and block_table.size(0) == B, "block_table batch mismatch")
     _require(seq_lens.dim() == 1 and seq_lens.size(0) == B, "seq_lens batch mismatch")
@@ -114,8 +152,7 @@ def stage1(q_rot, kv_cache, block_table, seq_lens, pair_lut, mid_o=None, *, num_
     rc = _lib.load().tq4_stage1_ex(
         q_rot.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
         pair_lut.data_ptr(), mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1),
-        kv_cache.stride(0), S, _layout_id(layout), scale, KERNELS[kernel], sinks_ptr,
-        _stream(q_rot.device))
+        stride, S, lid, scale, KERNELS[kernel], sinks_ptr, _stream(q_rot.device))
     _lib.check(rc, "tq4_stage1")
     return mid_o
 
@@ -172,7 +209,6 @@ def store(key, value, kv_cache, slot_mapping, rotation_t, midpoints, centroids=N
     _require(value.dtype == key.dtype and value.is_contiguous() and value.shape == key.shape,
              "value must match key (shape, dtype, contiguous)")
     _require(key.dim() == 3 and key.size(2) == HEAD_DIM, f"key must be [N, Hk, {HEAD_DIM}]")
-    _check_tensor(kv_cache, "kv_cache", torch.uint8)
     _check_tensor(slot_mapping, "slot_mapping", torch.int32)
     _check_tensor(rotation_t, "rotation_t", torch.float32)
     _check_tensor(midpoints, "midpoints", torch.float32)
@@ -184,8 +220,8 @@ def store(key, value, kv_cache, slot_mapping, rotation_t, midpoints, centroids=N
         _check_tensor(centroids, "centroids", torch.float32)
         _require(centroids.numel() == 16, "4-bit keys need 16 centroids")
     N, Hk, D = key.shape
-    _require(kv_cache.dim() == 4 and kv_cache.size(2) == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
-    _require(kv_cache.size(3) == slot_bytes(D), f"requires slot_size={slot_bytes(D)}")
+    bs, hk, stride, lid = _cache_geometry(kv_cache, slot_bytes(D), layout)
+    _require(hk == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
     _require(slot_mapping.numel() == N, "slot_mapping must have one entry per token")
     devs = {t.device for t in (key, value, kv_cache, slot_mapping, rotation_t, midpoints)}
     _require(len(devs) == 1, "all tensors must be on the same device")
@@ -193,8 +229,7 @@ def store(key, value, kv_cache, slot_mapping, rotation_t, midpoints, centroids=N
         key.data_ptr(), value.data_ptr(), DTYPES[key.dtype], slot_mapping.data_ptr(),
         rotation_t.data_ptr(), midpoints.data_ptr(),
         centroids.data_ptr() if centroids is not None else None, kv_cache.data_ptr(), N, Hk, D,
-        kv_cache.size(1), kv_cache.stride(0), _layout_id(layout), int(bool(norm_correction)),
-        _stream(key.device))
+        bs, stride, lid, int(bool(norm_correction)), _stream(key.device))
     _lib.check(rc, "tq4_store")
     return kv_cache
 
@@ -204,14 +239,12 @@ def stage1_fp8(query, kv_cache, block_table, seq_lens, mid_o=None, *, num_kv_spl
     """Stage1 of the FP8-key preset (``turboquant_k8v4``): ``query`` fp32 ``[B, Hq, D]``
     (not rotated), K one E4M3 byte per dim; returns ``mid_o [B, Hq, S, D+1]``.  ``kernel``:
     "auto" (16x16x32 MFMA where it applies, else VALU), "xdl" or "simple"."""
-    for t, n, dt in ((query, "query", torch.float32), (kv_cache, "kv_cache", torch.uint8),
-                     (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32)):
+    for t, n, dt in ((query, "query", torch.float32), (block_table, "block_table", torch.int32),
+                     (seq_lens, "seq_lens", torch.int32)):
         _check_tensor(t, n, dt)
     _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
     B, Hq, D = query.shape
-    _require(kv_cache.dim() == 4, "kv_cache must be [blocks, block_size, Hk, slot]")
-    _, bs, Hk, slot = kv_cache.shape
-    _require(slot == slot_bytes_fp8(D), f"requires slot_size={slot_bytes_fp8(D)} (FP8 keys)")
+    bs, Hk, stride, lid = _cache_geometry(kv_cache, slot_bytes_fp8(D), layout, " (FP8 keys)")
     _require(Hq % Hk == 0, "Hq must be a multiple of Hk")
     _require(block_table.dim() == 2 and block_table.size(0) == B, "block_table batch mismatch")
     _require(seq_lens.dim() == 1 and seq_lens.size(0) == B, "seq_lens batch mismatch")
@@ -228,9 +261,8 @@ def stage1_fp8(query, kv_cache, block_table, seq_lens, mid_o=None, *, num_kv_spl
     _require(kernel in ("auto", "xdl", "simple"), "kernel must be auto, xdl or simple")
     rc = _lib.load().tq4_stage1_fp8_ex(
         query.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
-        mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), kv_cache.stride(0), S,
-        _layout_id(layout), scale, _check_sinks(sinks, Hq, query.device), KERNELS[kernel],
-        _stream(query.device))
+        mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), stride, S, lid, scale,
+        _check_sinks(sinks, Hq, query.device), KERNELS[kernel], _stream(query.device))
     _lib.check(rc, "tq4_stage1_fp8")
     return mid_o
 
@@ -242,18 +274,16 @@ def store_fp8(key, value, kv_cache, slot_mapping, *, layout="soa"):
     _require(value.dtype == key.dtype and value.is_contiguous() and value.shape == key.shape,
              "value must match key (shape, dtype, contiguous)")
     _require(key.dim() == 3 and key.size(2) == HEAD_DIM, f"key must be [N, Hk, {HEAD_DIM}]")
-    _check_tensor(kv_cache, "kv_cache", torch.uint8)
     _check_tensor(slot_mapping, "slot_mapping", torch.int32)
     N, Hk, D = key.shape
-    _require(kv_cache.dim() == 4 and kv_cache.size(2) == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
-    _require(kv_cache.size(3) == slot_bytes_fp8(D), f"requires slot_size={slot_bytes_fp8(D)} (FP8 keys)")
+    bs, hk, stride, lid = _cache_geometry(kv_cache, slot_bytes_fp8(D), layout, " (FP8 keys)")
+    _require(hk == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
     _require(slot_mapping.numel() == N, "slot_mapping must have one entry per token")
     devs = {t.device for t in (key, value, kv_cache, slot_mapping)}
     _require(len(devs) == 1, "all tensors must be on the same device")
     rc = _lib.load().tq4_store_fp8(
         key.data_ptr(), value.data_ptr(), DTYPES[key.dtype], slot_mapping.data_ptr(),
-        kv_cache.data_ptr(), N, Hk, D, kv_cache.size(1), kv_cache.stride(0), _layout_id(layout),
-        _stream(key.device))
+        kv_cache.data_ptr(), N, Hk, D, bs, stride, lid, _stream(key.device))
     _lib.check(rc, "tq4_store_fp8")
     return kv_cache
 
@@ -265,21 +295,18 @@ def stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o=None,
                   value_bits, num_kv_splits=None, layout="soa", attn_scale=None, sinks=None,
                   kernel="auto"):
     """Stage1 of the bit-width presets (``turboquant_k3v4_nc``: 3/4, ``turboquant_3bit_nc``:
-    3/3, and 4/4) on the VALU kernel: ``q_rot`` fp32 ``[B, Hq, D]``, ``centroids`` the
-    ``2^key_bits`` Lloyd-Max centroids; returns ``mid_o [B, Hq, S, D+1]``.  ``kernel``:
-    "auto" (3/4 and 3/3 on the 16x16x32 MFMA kernel where it applies), "xdl" or "simple"."""
+    3/3, and 4/4): ``q_rot`` fp32 ``[B, Hq, D]``, ``centroids`` the ``2^key_bits`` Lloyd-Max
+    centroids; returns ``mid_o [B, Hq, S, D+1]``.  ``kernel``: "auto" (3/4 and 3/3 on the
+    16x16x32 MFMA kernel where it applies, 4/4 and other shapes on the VALU kernel), "xdl" or
+    "simple"."""
     _require((key_bits, value_bits) in PRESETS, f"key/value bits must be one of {PRESETS}")
-    for t, n, dt in ((q_rot, "q_rot", torch.float32), (kv_cache, "kv_cache", torch.uint8),
-                     (block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
-                     (centroids, "centroids", torch.float32)):
+    for t, n, dt in ((q_rot, "q_rot", torch.float32), (block_table, "block_table", torch.int32),
+                     (seq_lens, "seq_lens", torch.int32), (centroids, "centroids", torch.float32)):
         _check_tensor(t, n, dt)
     _require(q_rot.dim() == 3 and q_rot.size(2) == HEAD_DIM, f"q_rot must be [B, Hq, {HEAD_DIM}]")
     B, Hq, D = q_rot.shape
     _require(centroids.numel() == 1 << key_bits, f"{key_bits}-bit keys need {1 << key_bits} centroids")
-    _require(kv_cache.dim() == 4, "kv_cache must be [blocks, block_size, Hk, slot]")
-    _, bs, Hk, slot = kv_cache.shape
-    want = slot_bytes_preset(D, key_bits, value_bits)
-    _require(slot == want, f"requires slot_size={want}")
+    bs, Hk, stride, lid = _cache_geometry(kv_cache, slot_bytes_preset(D, key_bits, value_bits), layout)
     _require(Hq % Hk == 0, "Hq must be a multiple of Hk")
     _require(block_table.dim() == 2 and block_table.size(0) == B, "block_table batch mismatch")
     _require(seq_lens.dim() == 1 and seq_lens.size(0) == B, "seq_lens batch mismatch")
@@ -297,7 +324,7 @@ def stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o=None,
     rc = _lib.load().tq4_stage1_preset_ex(
         q_rot.data_ptr(), kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
         centroids.data_ptr(), mid_o.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1),
-        kv_cache.stride(0), S, _layout_id(layout), scale, _check_sinks(sinks, Hq, q_rot.device),
+        stride, S, lid, scale, _check_sinks(sinks, Hq, q_rot.device),
         key_bits, value_bits, KERNELS[kernel], _stream(q_rot.device))
     _lib.check(rc, "tq4_stage1_preset")
     return mid_o
@@ -312,7 +339,6 @@ def store_preset(key, value, kv_cache, slot_mapping, rotation_t, midpoints, cent
     _require(value.dtype == key.dtype and value.is_contiguous() and value.shape == key.shape,
              "value must match key (shape, dtype, contiguous)")
     _require(key.dim() == 3 and key.size(2) == HEAD_DIM, f"key must be [N, Hk, {HEAD_DIM}]")
-    _check_tensor(kv_cache, "kv_cache", torch.uint8)
     _check_tensor(slot_mapping, "slot_mapping", torch.int32)
     _check_tensor(rotation_t, "rotation_t", torch.float32)
     _check_tensor(midpoints, "midpoints", torch.float32)
@@ -325,9 +351,8 @@ def store_preset(key, value, kv_cache, slot_mapping, rotation_t, midpoints, cent
         _check_tensor(centroids, "centroids", torch.float32)
         _require(centroids.numel() == n_mid + 1, f"{key_bits}-bit keys need {n_mid + 1} centroids")
     N, Hk, D = key.shape
-    want = slot_bytes_preset(D, key_bits, value_bits)
-    _require(kv_cache.dim() == 4 and kv_cache.size(2) == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
-    _require(kv_cache.size(3) == want, f"requires slot_size={want}")
+    bs, hk, stride, lid = _cache_geometry(kv_cache, slot_bytes_preset(D, key_bits, value_bits), layout)
+    _require(hk == Hk, "kv_cache must be [blocks, block_size, Hk, slot]")
     _require(slot_mapping.numel() == N, "slot_mapping must have one entry per token")
     devs = {t.device for t in (key, value, kv_cache, slot_mapping, rotation_t, midpoints)}
     _require(len(devs) == 1, "all tensors must be on the same device")
@@ -335,8 +360,7 @@ def store_preset(key, value, kv_cache, slot_mapping, rotation_t, midpoints, cent
         key.data_ptr(), value.data_ptr(), DTYPES[key.dtype], slot_mapping.data_ptr(),
         rotation_t.data_ptr(), midpoints.data_ptr(),
         centroids.data_ptr() if centroids is not None else None, kv_cache.data_ptr(), N, Hk, D,
-        kv_cache.size(1), kv_cache.stride(0), _layout_id(layout), int(bool(norm_correction)),
-        key_bits, value_bits, _stream(key.device))
+        bs, stride, lid, int(bool(norm_correction)), key_bits, value_bits, _stream(key.device))
     _lib.check(rc, "tq4_store_preset")
     return kv_cache
 
@@ -363,13 +387,12 @@ def full_decode(query, rotation_t, kv_cache, block_table, seq_lens, centroids, n
     _check_tensor(rotation_t, "rotation_t", torch.float32)
     _check_tensor(centroids, "centroids", torch.float32)
     _require(centroids.numel() == 16, "4-bit path requires 16 centroids")
-    for t, n, dt in ((kv_cache, "kv_cache", torch.uint8), (block_table, "block_table", torch.int32),
-                     (seq_lens, "seq_lens", torch.int32)):
+    for t, n, dt in ((block_table, "block_table", torch.int32), (seq_lens, "seq_lens", torch.int32)):
         _check_tensor(t, n, dt)
+    _require(query.dim() == 3, "query must be [B, Hq, D]")
     B, Hq, D = query.shape
     _require(D == HEAD_DIM, f"requires D={HEAD_DIM}")
-    _, bs, Hk, slot = kv_cache.shape
-    _require(slot == slot_bytes(D), f"requires slot_size={slot_bytes(D)}")
+    bs, Hk, stride, lid = _cache_geometry(kv_cache, slot_bytes(D), layout)
     out_dtype = query.dtype if out_dtype is None else out_dtype
     ws = workspace or DecodeWorkspace(B, Hq, num_kv_splits, query.device, out_dtype)
     _require(ws.out.dtype == out_dtype and ws.mid_o.shape[:3] == (B, Hq, num_kv_splits),
@@ -380,8 +403,8 @@ def full_decode(query, rotation_t, kv_cache, block_table, seq_lens, centroids, n
         query.data_ptr(), DTYPES[query.dtype], rotation_t.data_ptr(), centroids.data_ptr(),
         kv_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), ws.q_rot.data_ptr(),
         ws.pair_lut.data_ptr(), ws.mid_o.data_ptr(), ws.out.data_ptr(), DTYPES[out_dtype],
-        ws.lse.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), kv_cache.stride(0),
-        num_kv_splits, _layout_id(layout), scale, sinks_ptr, _stream(query.device))
+        ws.lse.data_ptr(), B, Hq, Hk, D, bs, block_table.size(1), stride,
+        num_kv_splits, lid, scale, sinks_ptr, _stream(query.device))
     _lib.check(rc, "tq4_full_decode")
     return ws.out, ws.lse
 
@@ -396,43 +419,12 @@ def _buffer_view(buf, shape, dtype):
     return view if view.is_contiguous() else None
 
 
-def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, centroids, scale,
-                                mse_bits, key_packed_size, value_quant_bits, key_fp8=False,
-                                norm_correction=False, PiT=None, mid_o_buf=None, output_buf=None,
-                                lse_buf=None, buf_holder=None, max_num_kv_splits=32, sinks=None, *,
-                                layout="soa"):
-    """The decode entry of the vLLM backend (``reference/soa_decode_v1.py:485-643``; AoS
-    ``reference/aos_decode.py:486-626``): ``q_rot = query @ PiT``, pair LUT, Stage1 over
-    ``max_num_kv_splits`` splits, Stage2; returns ``[B, Hq, D]`` in the query dtype.
-
-    Caller buffers are used when they fit (``mid_o_buf`` fp32 ``[>=B, Hq, S, D+1]``,
-    ``output_buf`` ``[>=B, Hq, D]`` in the query dtype, ``lse_buf`` fp32 ``[>=B, Hq]``); the
-    rotated query and the pair LUT live on ``buf_holder`` when one is given; ``sinks``
-    (fp32 ``[Hq]``) enter split 0.  Built for the 4-bit ``turboquant_4bit_nc`` cache, with
-    ``key_fp8`` the ``turboquant_k8v4`` cache (unrotated query, VALU Stage1), and the 3-bit
-    presets ``turboquant_k3v4_nc`` / ``turboquant_3bit_nc`` (VALU Stage1); 4-bit AoS without
-    norm correction raises ``NotImplementedError``.
-    """
-    if key_fp8:
-        _require(value_quant_bits == 4, "FP8 keys are built with 4-bit values")
-        return _decode_attention_fp8(query, kv_cache, block_table, seq_lens, scale, key_packed_size,
-                                     mid_o_buf, output_buf, lse_buf, buf_holder, max_num_kv_splits,
-                                     sinks, layout)
-    _require((mse_bits, value_quant_bits) in PRESETS,
-             f"MSE key / value bits must be one of {PRESETS}")
-    if mse_bits != 4 or value_quant_bits != 4:
-        return _decode_attention_preset(query, kv_cache, block_table, seq_lens, Pi, PiT, centroids,
-                                        scale, mse_bits, key_packed_size, value_quant_bits,
-                                        norm_correction, mid_o_buf, output_buf, lse_buf, buf_holder,
-                                        max_num_kv_splits, sinks, layout)
-    _require(key_packed_size == HEAD_DIM // 2 + 2, f"key_packed_size must be {HEAD_DIM // 2 + 2}")
-    if layout == "aos" and not norm_correction:
-        raise NotImplementedError("AoS decode is built with the norm correction (turboquant_4bit_nc)")
-    _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
+def _decode_buffers(query, S, buf_holder, mid_o_buf, output_buf, lse_buf):
+    """Workspace of one decode call: the caller's ``mid_o_buf`` / ``output_buf`` /
+    ``lse_buf`` when they fit (leading sub-blocks, as ``reference/soa_decode_v1.py:541-560``
+    takes them), else buffers kept on ``buf_holder`` and reused by later calls of the same
+    shape, so that a captured call replays on the same memory."""
     B, Hq, D = query.shape
-    S = int(max_num_kv_splits)
-    if PiT is None:
-        PiT = Pi.t().contiguous()
     dev = query.device
 
     def held(name, shape, dtype):
@@ -444,78 +436,73 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
                 setattr(buf_holder, name, view)
         return view
 
+    def given(buf, name, shape, dtype):
+        view = _buffer_view(buf, shape, dtype)
+        return view if view is not None else held(name, shape, dtype)
+
     ws = DecodeWorkspace.__new__(DecodeWorkspace)
     ws.q_rot = held("_tq4_q_rot_buf", (B, Hq, D), torch.float32)
     ws.pair_lut = held("_tq4_pair_lut_buf", (256, 2), torch.float32)
-    ws.mid_o = _buffer_view(mid_o_buf, (B, Hq, S, D + 1), torch.float32)
-    if ws.mid_o is None:
-        ws.mid_o = held("_tq_mid_o_buf", (B, Hq, S, D + 1), torch.float32)
-    ws.out = _buffer_view(output_buf, (B, Hq, D), query.dtype)
-    if ws.out is None:
-        ws.out = held("_tq_output_buf", (B, Hq, D), query.dtype)
-    ws.lse = _buffer_view(lse_buf, (B, Hq), torch.float32)
-    if ws.lse is None:
-        ws.lse = held("_tq_lse_buf", (B, Hq), torch.float32)
-    out, _ = full_decode(query.contiguous(), PiT, kv_cache, block_table, seq_lens, centroids, S,
-                         layout=layout, out_dtype=query.dtype, attn_scale=scale, workspace=ws,
-                         sinks=sinks)
-    return out
+    ws.mid_o = given(mid_o_buf, "_tq_mid_o_buf", (B, Hq, S, D + 1), torch.float32)
+    ws.out = given(output_buf, "_tq_output_buf", (B, Hq, D), query.dtype)
+    ws.lse = given(lse_buf, "_tq_lse_buf", (B, Hq), torch.float32)
+    return ws
 
 
-def _decode_attention_preset(query, kv_cache, block_table, seq_lens, Pi, PiT, centroids, scale,
-                             mse_bits, key_packed_size, value_quant_bits, norm_correction,
-                             mid_o_buf, output_buf, lse_buf, buf_holder, max_num_kv_splits, sinks,
-                             layout):
-    """3-bit-key presets: ``q_rot = query @ PiT`` on the matrix cores, VALU Stage1, Stage2."""
-    if layout == "aos" and not norm_correction:
-        raise NotImplementedError("AoS decode is built with the norm correction (the _nc presets)")
+def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, centroids, scale,
+                                mse_bits, key_packed_size, value_quant_bits, key_fp8=False,
+                                norm_correction=False, PiT=None, mid_o_buf=None, output_buf=None,
+                                lse_buf=None, buf_holder=None, max_num_kv_splits=32, sinks=None, *,
+                                layout="soa"):
+    """The decode entry of the vLLM backend (``reference/soa_decode_v1.py:485-643``; AoS
+    ``reference/aos_decode.py:486-626``): ``q_rot = query @ PiT``, pair LUT, Stage1 over
+    ``max_num_kv_splits`` splits, Stage2; returns ``[B, Hq, D]`` in the query dtype.
+
+    ``kv_cache`` is the contiguous ``[blocks, block_size, Hk, slot]`` cache or the backend's
+    ``transpose(1, 2)`` view of its ``[blocks, Hk, block_size, slot]`` cache.  Caller buffers
+    are used when they fit (``mid_o_buf`` fp32 ``[>=B, Hq, S, D+1]``, ``output_buf``
+    ``[>=B, Hq, D]`` in the query dtype, ``lse_buf`` fp32 ``[>=B, Hq]``); the other buffers
+    live on ``buf_holder`` when one is given.  The launches depend only on shapes, never on
+    ``seq_lens`` or ``block_table`` contents, and nothing is allocated once ``buf_holder``
+    holds the buffers, so a call can be captured in a graph and replayed
+    (``reference/turboquant_attn.py:368-373``).  ``sinks`` (fp32 ``[Hq]``) enter split 0.
+    Built for the 4-bit ``turboquant_4bit_nc`` cache, with ``key_fp8`` the ``turboquant_k8v4``
+    cache (unrotated query), and the 3-bit presets ``turboquant_k3v4_nc`` /
+    ``turboquant_3bit_nc``, all on the 16x16x32 MFMA Stage1 where it applies (GQA 4 or 8),
+    else the VALU kernel; 4-bit AoS without norm correction raises ``NotImplementedError``.
+    """
+    _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
+    S = int(max_num_kv_splits)
+    ws = _decode_buffers(query, S, buf_holder, mid_o_buf, output_buf, lse_buf)
+    if key_fp8:
+        _require(value_quant_bits == 4, "FP8 keys are built with 4-bit values")
+        _require(key_packed_size == HEAD_DIM, f"key_packed_size must be {HEAD_DIM} for FP8 keys")
+        # the unrotated query (reference/soa_decode_v1.py:528-534), as fp32
+        ws.q_rot.copy_(query)
+        stage1_fp8(ws.q_rot, kv_cache, block_table, seq_lens, ws.mid_o, layout=layout,
+                   attn_scale=scale, sinks=sinks)
+        stage2(ws.mid_o, seq_lens, ws.out, ws.lse)
+        return ws.out
+    _require((mse_bits, value_quant_bits) in PRESETS,
+             f"MSE key / value bits must be one of {PRESETS}")
     want = HEAD_DIM * mse_bits // 8 + 2
     _require(key_packed_size == want, f"key_packed_size must be {want}")
-    _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
-    B, Hq, D = query.shape
-    S = int(max_num_kv_splits)
+    if layout == "aos" and not norm_correction:
+        raise NotImplementedError("AoS decode is built with the norm correction (the _nc presets)")
     if PiT is None:
         PiT = Pi.t().contiguous()
-    q_rot = rotate_query(query.contiguous(), PiT)
-    mid_o = _buffer_view(mid_o_buf, (B, Hq, S, D + 1), torch.float32)
-    if mid_o is None:
-        mid_o = torch.empty(B, Hq, S, D + 1, dtype=torch.float32, device=query.device)
-        if buf_holder is not None:
-            buf_holder._tq_mid_o_buf = mid_o
-    out = _buffer_view(output_buf, (B, Hq, D), query.dtype)
-    if out is None:
-        out = torch.empty(B, Hq, D, dtype=query.dtype, device=query.device)
-    lse = _buffer_view(lse_buf, (B, Hq), torch.float32)
-    if lse is None:
-        lse = torch.empty(B, Hq, dtype=torch.float32, device=query.device)
-    stage1_preset(q_rot, kv_cache, block_table, seq_lens, centroids.float().contiguous(), mid_o,
-                  key_bits=mse_bits, value_bits=value_quant_bits, layout=layout, attn_scale=scale,
-                  sinks=sinks)
-    stage2(mid_o, seq_lens, out, lse, out_dtype=query.dtype)
-    return out
-
-
-def _decode_attention_fp8(query, kv_cache, block_table, seq_lens, scale, key_packed_size,
-                          mid_o_buf, output_buf, lse_buf, buf_holder, max_num_kv_splits, sinks,
-                          layout):
-    """FP8-key decode (``reference/soa_decode_v1.py:528-534`` passes the query unrotated)."""
-    _require(key_packed_size == HEAD_DIM, f"key_packed_size must be {HEAD_DIM} for FP8 keys")
-    B, Hq, D = query.shape
-    S = int(max_num_kv_splits)
-    mid_o = _buffer_view(mid_o_buf, (B, Hq, S, D + 1), torch.float32)
-    if mid_o is None:
-        mid_o = torch.empty(B, Hq, S, D + 1, dtype=torch.float32, device=query.device)
-        if buf_holder is not None:
-            buf_holder._tq_mid_o_buf = mid_o
-    out = _buffer_view(output_buf, (B, Hq, D), query.dtype)
-    if out is None:
-        out = torch.empty(B, Hq, D, dtype=query.dtype, device=query.device)
-    lse = _buffer_view(lse_buf, (B, Hq), torch.float32)
-    if lse is None:
-        lse = torch.empty(B, Hq, dtype=torch.float32, device=query.device)
-    stage1_fp8(query.float().contiguous(), kv_cache, block_table, seq_lens, mid_o, layout=layout,
-               attn_scale=scale, sinks=sinks)
-    stage2(mid_o, seq_lens, out, lse, out_dtype=query.dtype)
+    query = query.contiguous()
+    if mse_bits != 4 or value_quant_bits != 4:
+        # 3-bit-key presets: rotation, Stage1 over the preset cache, Stage2
+        rotate_query(query, PiT, ws.q_rot)
+        stage1_preset(ws.q_rot, kv_cache, block_table, seq_lens, centroids.float().contiguous(),
+                      ws.mid_o, key_bits=mse_bits, value_bits=value_quant_bits, layout=layout,
+                      attn_scale=scale, sinks=sinks)
+        stage2(ws.mid_o, seq_lens, ws.out, ws.lse)
+        return ws.out
+    out, _ = full_decode(query, PiT, kv_cache, block_table, seq_lens, centroids, S,
+                         layout=layout, out_dtype=query.dtype, attn_scale=scale, workspace=ws,
+                         sinks=sinks)
     return out
 
 
@@ -594,15 +581,13 @@ class _CudaExtCompat:
 
     ``tq4_cuda_vN(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o)`` runs the SoA
     Stage1 with the split count taken from ``mid_o``; ``tq4_cuda_v7_stage2(mid_o, output,
-    lse)`` takes ``seq_lens`` from the last Stage1 call's argument when not given, as the
-    reference kernel has no ``seq_lens`` argument; ``tq4_cuda_v7_full`` runs both.
+    lse)`` merges every split of every row, as the reference V7 kernel does
+    (``cuda/tq4_cuda_v7.cu:44-47``; it has no ``seq_lens`` argument), or only the non-empty
+    splits when ``seq_lens`` is given; ``tq4_cuda_v7_full`` runs Stage1 and Stage2.  The
+    object holds no state between calls.
     """
 
-    def __init__(self):
-        self._last_seq_lens = None
-
     def _stage1(self, q_rot, kv_cache, block_table, seq_lens, centroids, mid_o):
-        self._last_seq_lens = seq_lens
         return launch_soa_v1_stage1(q_rot, kv_cache, block_table, seq_lens, centroids, mid_o)
 
     def __getattr__(self, name):
@@ -614,10 +599,11 @@ class _CudaExtCompat:
         return self._stage1(*args)
 
     def tq4_cuda_v7_stage2(self, mid_o, output, lse, seq_lens=None):
-        sl = seq_lens if seq_lens is not None else self._last_seq_lens
-        if sl is None:
-            sl = torch.full((mid_o.size(0),), mid_o.size(2), dtype=torch.int32, device=mid_o.device)
-        stage2(mid_o, sl, output, lse)
+        if seq_lens is None:
+            # a length of S tokens over S splits makes every split non-empty
+            seq_lens = torch.full((mid_o.size(0),), mid_o.size(2), dtype=torch.int32,
+                                  device=mid_o.device)
+        stage2(mid_o, seq_lens, output, lse)
         return output
 
     def tq4_cuda_v7_full(self, q_rot, kv_cache, block_table, seq_lens, centroids, mid_o, output,
