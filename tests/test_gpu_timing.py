@@ -40,7 +40,10 @@ def test_next_launch_stamps_kernel_interval(dev):
     around = ms.value
     print(f"kernel {kernel * 1e3:.2f} us, around {around * 1e3:.2f} us")
     assert 0 < kernel <= around
-    # never-recorded events: hipEventElapsedTime reports an error
+    # never-recorded events: hipEventElapsedTime reports an error, which stays the thread's
+    # last HIP error until read: read it here, or the next torch call reports it
     assert hip.hipEventElapsedTime(ctypes.byref(ms), ka2, kb2) != 0
+    assert hip.hipGetLastError() != 0
+    assert hip.hipGetLastError() == 0
     for e in ev:
         hip.hipEventDestroy(e)
