@@ -121,6 +121,25 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
                     float attn_scale, const float *sinks, tq4_stream_t stream);
 
 /*
+ * tq4_full_decode without caller workspaces: the pair LUT, the rotated queries and the
+ * Stage1 rows live in a 40 MiB device array the library holds on every GPU it runs on (from
+ * its load until the process ends), so the call allocates nothing -- no hipMalloc, no
+ * allocator.  Shapes whose workspace exceeds the array (2 KiB LUT + B*Hq*D*4 bytes of
+ * q_rot + B*Hq*S*(D+1)*4 bytes of Stage1 rows unless one split per sequence applies) are
+ * rejected with TQ4_E_INVALID.  Calls that overlap on one GPU share the array and race:
+ * serialize them (one stream, or events).  Otherwise as tq4_full_decode.
+ * No counterpart in the reference: for callers that cannot allocate (code under graph
+ * capture, tight serving loops, harnesses that forbid allocation).
+ */
+int tq4_full_decode_noalloc(const void *query, int query_dtype, const float *rot_t,
+                            const float *centroids, const uint8_t *kv_cache,
+                            const int32_t *block_table, const int32_t *seq_lens, void *out,
+                            int out_dtype, float *lse, int B, int Hq, int Hk, int D,
+                            int block_size, int max_blocks_per_seq, int64_t cache_block_stride,
+                            int num_kv_splits, int layout, float attn_scale, const float *sinks,
+                            tq4_stream_t stream);
+
+/*
  * Cache writer: quantize key / value [N, Hk, D] (dtype TQ4_F32 / TQ4_BF16 / TQ4_F16,
  * contiguous, 16-byte aligned) and write token i into cache slot slot_mapping[i]
  * (block slot / block_size, position slot % block_size; slots < 0 are skipped).  K:

@@ -8,6 +8,7 @@
 #include <hip/hip_ext.h>
 #include <atomic>
 #include <cstdarg>
+#include <mutex>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -363,6 +364,48 @@ int launch_store(const void *key, const void *value, int dtype, const int32_t *s
     return launch_status(what);
 }
 
+// Workspace of tq4_full_decode_noalloc in device memory the library owns: the pair LUT,
+// the rotated queries and (unless one split per sequence applies) the Stage1 rows.  One
+// copy per GPU the library runs on, held from the code object's load until the process
+// ends; calls that overlap on one GPU share it and race.  Nothing in it has to start at
+// zero: the rotation launch writes the LUT and q_rot before Stage1 reads them, and Stage2
+// reads only the rows of non-empty splits, which Stage1 writes.
+constexpr size_t kScratchBytes = size_t(40) << 20;
+constexpr size_t kScratchAlign = 256;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per device (the host
+// symbol is only a handle for the lookup).
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_address(void **ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return fail((int)e, "tq4_full_decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_full_decode_noalloc: device %d beyond the %d the library tracks", dev,
+                    kMaxDevices);
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p)
+                return fail(e != hipSuccess ? (int)e : TQ4_E_INVALID,
+                            "tq4_full_decode_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *ptr = p;
+    return TQ4_OK;
+}
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
 }  // namespace
 
 extern "C" {
@@ -530,6 +573,44 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
     if (rc)
         return rc;
     return tq4_stage2(mid_o, seq_lens, out, out_dtype, lse, B, Hq, D, a.S, stream);
+}
+
+int tq4_full_decode_noalloc(const void *query, int query_dtype, const float *rot_t,
+                            const float *centroids, const uint8_t *kv_cache,
+                            const int32_t *block_table, const int32_t *seq_lens, void *out,
+                            int out_dtype, float *lse, int B, int Hq, int Hk, int D,
+                            int block_size, int max_blocks_per_seq, int64_t cache_block_stride,
+                            int num_kv_splits, int layout, float attn_scale, const float *sinks,
+                            tq4_stream_t stream) {
+    if (B <= 0 || Hq <= 0 || num_kv_splits <= 0)
+        return fail(TQ4_E_INVALID, "tq4_full_decode_noalloc: B, Hq and num_kv_splits must be positive");
+    if (D != tq4::kHeadDim)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_full_decode_noalloc: head_dim %d unsupported (128)", D);
+    void *base = nullptr;
+    int rc = scratch_address(&base);
+    if (rc)
+        return rc;
+    // scratch layout: pair LUT | q_rot [B, Hq, D] | mid_o [B, Hq, S, D + 1] (only when Stage1
+    // runs more than one split per sequence), each 256-byte aligned
+    unsigned char *bytes = static_cast<unsigned char *>(base);
+    const size_t lut_bytes = round_up(256 * 2 * sizeof(float), kScratchAlign);
+    const size_t q_bytes = round_up((size_t)B * Hq * D * sizeof(float), kScratchAlign);
+    float *lut = reinterpret_cast<float *>(bytes);
+    float *q_rot = reinterpret_cast<float *>(bytes + lut_bytes);
+    float *mid_o = reinterpret_cast<float *>(bytes + lut_bytes + q_bytes);
+    Stage1Args a{q_rot, kv_cache, block_table, seq_lens, lut, mid_o, B, Hq, Hk, D, block_size,
+                 max_blocks_per_seq, cache_block_stride, num_kv_splits, layout, attn_scale, sinks};
+    const bool one_split = check_stage1(a) == TQ4_OK && auto_xdl_waves(a) == 1;
+    const size_t mid_bytes = one_split ? 0 : (size_t)B * Hq * num_kv_splits * (D + 1) * sizeof(float);
+    const size_t need = lut_bytes + q_bytes + mid_bytes;
+    if (need > kScratchBytes)
+        return fail(TQ4_E_INVALID,
+                    "tq4_full_decode_noalloc: B=%d Hq=%d S=%d needs %zu bytes of workspace (q_rot %zu, "
+                    "mid_o %zu), the library's scratch holds %zu",
+                    B, Hq, num_kv_splits, need, q_bytes, mid_bytes, kScratchBytes);
+    return tq4_full_decode(query, query_dtype, rot_t, centroids, kv_cache, block_table, seq_lens, q_rot, lut,
+                           mid_o, out, out_dtype, lse, B, Hq, Hk, D, block_size, max_blocks_per_seq,
+                           cache_block_stride, num_kv_splits, layout, attn_scale, sinks, stream);
 }
 
 int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot_mapping,

@@ -23,6 +23,7 @@ EXPORTS = (
     "tq4_rotate_query",
     "tq4_build_pair_lut",
     "tq4_full_decode",
+    "tq4_full_decode_noalloc",
     "tq4_store",
     "tq4_stage1_fp8",
     "tq4_stage1_fp8_ex",
@@ -46,6 +47,8 @@ _SIGS = {
     "tq4_build_pair_lut": [_p, _p, _i, _p],
     "tq4_full_decode": [_p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i,
                         _i, _i64, _i, _i, _f, _p, _p],
+    "tq4_full_decode_noalloc": [_p, _i, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i,
+                                _i64, _i, _i, _f, _p, _p],
     "tq4_store": [_p, _p, _i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _p],
     "tq4_last_error": [],
     "tq4_abi_version": [],
