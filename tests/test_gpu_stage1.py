@@ -153,6 +153,28 @@ def test_xdl_on_store_written_cache_full_size(dev, layout):
     assert_parity(got, ref, 1e-5)
 
 
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("group", [4, 8])
+def test_wave_deal_over_several_lane_chunks(dev, layout, group):
+    # 150 sequences (three 64-lane chunks of the kernel's wave deal), about a third empty,
+    # lengths 1 .. 700: every live split is written once, every dead one stays NaN
+    rng = np.random.default_rng(109)
+    lens = rng.integers(1, 700, size=150)
+    lens[rng.random(150) < 0.33] = 0
+    hk = 2 if group == 8 else 4
+    w = workloads.small(109, 150, lens, 32, num_q_heads=hk * group, num_kv_heads=hk)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, hk) if layout == "aos" else None
+    assert_parity(run(w, dev, "xdl", layout, cache), oracle(w, layout, cache))
+
+
+def test_wave_deal_gives_a_lone_long_sequence_many_waves(dev):
+    # two live sequences out of 64: the deal hands the long one up to one wave per split
+    lens = [0] * 64
+    lens[5], lens[40] = 4096, 33
+    w = workloads.small(110, 64, lens, 32)
+    assert_parity(run(w, dev, "xdl"), oracle(w))
+
+
 def test_xdl_ragged_and_gqa8_full_size(dev):
     for w in (workloads.ragged_b64(), workloads.gqa8_b8_ctx32768()):
         assert_parity(run(w, dev, "xdl"), oracle(w))

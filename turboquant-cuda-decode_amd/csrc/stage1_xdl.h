@@ -371,6 +371,85 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
     return r;
 }
 
+// Waves of one kv-head dealt to the sequences.  The grid gives every kv-head nw * B
+// waves (wave x = wid + nw * b), a number fixed by the shapes alone.  A sequence with live
+// splits gets one wave plus a share of the other nw * B - n_live in proportion to its
+// estimated stream length (prefix rounding: the shares sum to exactly that many), and at
+// most one wave per live split; each wave then takes an equal run of its sequence's live
+// splits.  Every wave of the kv-head computes the same deal from seq_lens, so ragged
+// batches keep the waves about equally busy; equal lengths give every sequence nw waves
+// (taken without the arithmetic).
+struct Deal {
+    int b, wid, nw;  // b < 0: the deal leaves this wave without work
+};
+
+// Live splits and estimated stream positions of sequence bb (0 past the batch): each
+// split's tiles (one more when it straddles a tile edge), as the stream pads them.
+struct SeqLoad {
+    int live;
+    uint32_t est;
+};
+__device__ __forceinline__ SeqLoad sequence_load(const int32_t *__restrict__ seq_lens, int B, int S, int bb) {
+    const int len = bb < B ? max(seq_lens[bb], 0) : 0;
+    const int split_len = (len + S - 1) / S;
+    const int live = split_len > 0 ? (len + split_len - 1) / split_len : 0;
+    return SeqLoad{live, (uint32_t)live * (uint32_t)(((split_len + 15) >> 4) + 1)};
+}
+
+// Inclusive prefix sum over the wave's 64 lanes: shifts within each 16-lane row, then the
+// row totals broadcast into the rows after them.
+__device__ __forceinline__ uint32_t wave_scan(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);   // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);   // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);   // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);   // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
+// Stream totals stay far below 2^32: a position covers 16 tokens of one kv-head.
+__device__ Deal deal_waves(const int32_t *__restrict__ seq_lens, int B, int S, int nw, int x, int lane) {
+    // equal lengths: every sequence keeps its nw waves, as the deal would give them
+    const int len0 = seq_lens[0];
+    bool equal = true;
+    for (int c0 = 0; c0 < B; c0 += kWave) {
+        const int bb = c0 + lane;
+        equal = equal && __ballot(bb < B && seq_lens[bb] != len0) == 0;
+    }
+    if (equal)
+        return Deal{x / nw, x % nw, nw};
+    const SeqLoad first = sequence_load(seq_lens, B, S, lane);
+    uint32_t est_total = 0;
+    int n_live = 0;
+    for (int c0 = 0; c0 < B; c0 += kWave) {
+        const SeqLoad q = c0 == 0 ? first : sequence_load(seq_lens, B, S, c0 + lane);
+        est_total += (uint32_t)__builtin_amdgcn_readlane((int)wave_scan(q.est), kWave - 1);
+        n_live += __builtin_popcountll(__ballot(q.live > 0));
+    }
+    const double spare = (double)((int64_t)nw * B - n_live);
+    // spare waves dealt to the sequences before prefix p: floor(spare * p / total), exact in
+    // double (the quotient of integers below 2^53 lands on an integer only when it is one)
+    auto cut = [&](uint32_t p) { return est_total > 0 ? (int)floor(spare * (double)p / (double)est_total) : 0; };
+    uint32_t est_carry = 0;
+    int wave_carry = 0;
+    for (int c0 = 0; c0 < B; c0 += kWave) {
+        const SeqLoad q = c0 == 0 ? first : sequence_load(seq_lens, B, S, c0 + lane);
+        const uint32_t est_out = est_carry + wave_scan(q.est);
+        const int mine = q.live > 0 ? min(1 + cut(est_out) - cut(est_out - q.est), q.live) : 0;
+        const int w_out = wave_carry + (int)wave_scan((uint32_t)mine);
+        const int w_in = w_out - mine;
+        const uint64_t hit = __ballot(x >= w_in && x < w_out);
+        if (hit) {
+            const int l = __builtin_ctzll(hit);
+            return Deal{c0 + l, x - __builtin_amdgcn_readlane(w_in, l), __builtin_amdgcn_readlane(mine, l)};
+        }
+        est_carry = (uint32_t)__builtin_amdgcn_readlane((int)est_out, kWave - 1);
+        wave_carry = __builtin_amdgcn_readlane(w_out, kWave - 1);
+    }
+    return Deal{-1, 0, 0};
+}
+
 // Running softmax state of a lane: the shared max of its head (as -m, exp2 domain;
 // +FLT_MAX = "no token yet"), the lane's own partial sums.
 struct State {
@@ -887,23 +966,32 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         }
     }
     const int lane = threadIdx.x;
-    // The pair-LUT rows and q do not depend on the sequence length: they go out first, the
-    // K table and the q operands are built once the first tiles' loads are on their way.
+    // The pair-LUT rows do not depend on the sequence: they go out first; the K table and the
+    // q operands are built once the first tiles' loads are on their way.
     static_assert(!(KF8 && KB3), "one key format");
     static_assert(!V3 || (KB3 && !FUSED), "3-bit values come with 3-bit keys, not fused");
     using RK = std::conditional_t<KF8, RawK8, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>;
     LutRows lut_rows{};
     if constexpr (!KF8 && !KB3)
         lut_rows = load_lut_rows(pair_lut, lane);
+    int run_waves = nw;  // waves sharing this wave's sequence and kv-head
+    if constexpr (!FUSED) {
+        const Deal d = deal_waves(seq_lens, gridDim.z, num_splits, nw, wid + nw * b, lane);
+        if (d.b < 0)
+            return;
+        b = d.b;
+        wid = d.wid;
+        run_waves = d.nw;
+    }
     float4 q_rows[8];
     load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + kvh * G + ((lane & 15) & (G - 1)), lane >> 4, KF8);
     const int seq_len = seq_lens[b];
     // split partition: L = ceil(len / S); live splits are those with s * L < len
     const int split_len = (seq_len + num_splits - 1) / num_splits;
-    // wave x of the W waves of this (sequence, kv-head) takes splits [x * S / W, (x + 1) * S / W)
-    const int s_lo = (int)((int64_t)wid * num_splits / nw);
     const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
-    const int s_hi = min((int)((int64_t)(wid + 1) * num_splits / nw), live);
+    // wave x of the W waves of this (sequence, kv-head) takes live splits [x * live / W, (x + 1) * live / W)
+    const int s_lo = (int)((int64_t)wid * live / run_waves);
+    const int s_hi = (int)((int64_t)(wid + 1) * live / run_waves);
     if constexpr (FUSED) {
         if (live == 0) {
             // an empty sequence: what Stage2 writes for it (0 / 0 and ln 0)
