@@ -18,8 +18,8 @@
 //
 // A workgroup of 8 waves stages 16 * PiT^T in LDS as f16 hi + lo parts once, then its
 // waves walk the rows 16 at a time (grid-stride); the first tile's K and V loads are issued
-// before the staging, each later tile's at the end of the previous one (fp32 V, 32 VGPRs,
-// where it is used).  Lane (n, g) = (lane % 16, lane / 16) loads dims 32g .. 32g+31 of
+// right after the staging's own loads, each later tile's at the end of the previous one
+// (fp32 V, 32 VGPRs, where it is used).  Lane (n, g) = (lane % 16, lane / 16) loads dims 32g .. 32g+31 of
 // row n of K and V.  The rotation is the transposed product
 // y^T = PiT^T x_hat^T on v_mfma_f32_16x16x32_f16, with operands and x_hat (scaled by 16,
 // keeping the lo parts out of f16 denormals) split into f16 hi + lo (products hi*hi +
@@ -203,7 +203,37 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
     const int stride = gridDim.x * kWaves;
     int tile = blockIdx.x * kWaves + wave;
 
-    // the first tile's K and V loads go out before the staging below
+    // Every workgroup reads PiT, the midpoints and the centroids (L2 hits after the first
+    // workgroup): their loads go out ahead of the first tile's K and V.  Those reads, across
+    // the grid, keep HBM busy for microseconds, and a staging load queued behind them would
+    // hold the workgroup's staging, and with it every wave's first tile, until they drain.
+    // (centroids may be null without norm correction: read only with it)
+    constexpr int kCents = 1 << KB;
+    float mid[kMids], cent[kCents];
+#pragma unroll
+    for (int i = 0; i < kMids; ++i)
+        mid[i] = midpoints[i];
+#pragma unroll
+    for (int i = 0; i < kCents; ++i)
+        cent[i] = 0.f;
+    if (norm_correction) {
+#pragma unroll
+        for (int i = 0; i < kCents; ++i)
+            cent[i] = centroids[i];
+    }
+    // thread (c, k8): 16 * PiT[8k8 .. 8k8+7][c] (coalesced over c) -> one 16-byte LDS write
+    // into each part
+    constexpr int kStage = kHeadDim * (kHeadDim / 8) / (kWave * kWaves);
+    float pw[kStage][8];
+#pragma unroll
+    for (int it = 0; it < kStage; ++it) {
+        const int i = threadIdx.x + it * kWave * kWaves;
+        const int c = i % kHeadDim, k8 = i / kHeadDim;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            pw[it][j] = pit[(8 * k8 + j) * kHeadDim + c];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     constexpr bool kEarlyV = sizeof(T) < 4;
     Chunk<T> kr, vr;
     {
@@ -212,29 +242,32 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
         if constexpr (kEarlyV)
             load_raw(vr, value + row * kHeadDim + 32 * g, row < rows);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // thread (c, k8): 16 * PiT[8k8 .. 8k8+7][c] (coalesced over c) -> one 16-byte LDS write
-    // into each part
 #pragma unroll
-    for (int it = 0; it < kHeadDim * (kHeadDim / 8) / (kWave * kWaves); ++it) {
+    for (int it = 0; it < kStage; ++it) {
         const int i = threadIdx.x + it * kWave * kWaves;
         const int c = i % kHeadDim, k8 = i / kHeadDim;
         half8 h, l;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float w = 16.f * pit[(8 * k8 + j) * kHeadDim + c];
+            const float w = 16.f * pw[it][j];
             h[j] = (_Float16)w;
             l[j] = (_Float16)(w - (float)h[j]);
         }
         *reinterpret_cast<half8 *>(pt_hi + pt_off(c, k8)) = h;
         *reinterpret_cast<half8 *>(pt_lo + pt_off(c, k8)) = l;
     }
-    if (threadIdx.x <= kMids)
-        c2tab[threadIdx.x] = norm_correction ? centroids[threadIdx.x] * centroids[threadIdx.x] : 0.f;
-    float mid[kMids];
+    // c[idx]^2 (0 without norm correction) of a lane's index, selected from the registers
+    auto c2_at = [&](int idx) {
+        float r = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMids; ++i)
-        mid[i] = midpoints[i];
+        for (int i = 0; i < kCents; ++i)
+            r = idx == i ? cent[i] * cent[i] : r;
+        return norm_correction ? r : 0.f;
+    };
+    if (threadIdx.x <= kMids)
+        c2tab[threadIdx.x] = c2_at(threadIdx.x);
     float mmin = mid[0], mmax = mid[0];
 #pragma unroll
     for (int i = 1; i < kMids; ++i) {
@@ -260,9 +293,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
         cell_ok = inside <= 1 && w > 0.f && w < __builtin_inff();
         const int up = base < kMids ? base + 1 : kMids;
         // the midpoint is stored x 256, the scale of the rotation's results
-        btab[k] = float4{256.f * m_in, __builtin_bit_cast(float, base),
-                         norm_correction ? centroids[base] * centroids[base] : 0.f,
-                         norm_correction ? centroids[up] * centroids[up] : 0.f};
+        btab[k] = float4{256.f * m_in, __builtin_bit_cast(float, base), c2_at(base), c2_at(up)};
     }
     const bool use_cells = __syncthreads_and(cell_ok) != 0;
     // cell coordinate (y - y0) / w of y = acc / 256
