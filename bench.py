@@ -68,8 +68,8 @@ def traffic_from_profile(name: str):
     path = PROFILES / f"{name}_pmc.md"
     if not path.exists():
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", path.read_text())
-    return float(m.group(1)) if m else None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9][0-9,.]*)", path.read_text())
+    return float(m.group(1).replace(",", "")) if m else None
 
 
 class HipEvents:
@@ -421,6 +421,59 @@ def side_workload(args, dev) -> int:
         metric = f"cache writer ({entry}, SoA, bf16 K/V, 8 kv-heads) {size}: GB/s"
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = "bf16 in, f32 math"
+    elif args.workload in ("stage1_ragged_b64", "stage1_gqa8_b8_ctx32768"):
+        from tq4_decode import workloads
+
+        w = workloads.ragged_b64() if args.workload == "stage1_ragged_b64" else workloads.gqa8_b8_ctx32768()
+        r = stage1_workload_time(dev, flush, timer, w, reps=args.steps)
+        us, gbs = r["us"], r["GBps"]
+        metric = {"stage1_ragged_b64": "Stage1, B64 ragged (seq_lens 512..8192), 32/8 heads, 32 splits: GB/s",
+                  "stage1_gqa8_b8_ctx32768": "Stage1, B8 x ctx32768, 64/8 heads (GQA-8), 64 splits: GB/s"}[
+            args.workload]
+        timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
+        dtype = "4-bit K/V, f32 math"
+    elif args.workload == "stage1_l2_resident":
+        import numpy as np
+
+        from tq4_decode import ops, workloads
+
+        # the headline launch with every sequence's block table pointing at the same 16 KV
+        # blocks (274 KB, resident in every XCD's L2 after one launch): what the kernel costs
+        # when HBM is taken out of the picture
+        w = workloads.qwen3_4b_b64_ctx4096()
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        q, c, sl, lut = t(w.q_rot), t(w.kv_cache), t(w.seq_lens), t(w.pair_lut)
+        bt16 = (torch.arange(w.block_table.shape[1], dtype=torch.int32, device=dev) % 16).repeat(w.batch, 1)
+        mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
+        times = []
+        for i in range(args.steps + 3):
+            ops.stage1(q, c, bt16, sl, lut, mid)  # warms L2 with the 16 blocks
+            a, b = timer.pair()
+            timer.stamp_next_launch(a, b)
+            ops.stage1(q, c, bt16, sl, lut, mid)
+            torch.cuda.synchronize()
+            if i >= 3:
+                times.append(timer.elapsed_ms(a, b) * 1e3)
+            timer.destroy(a, b)
+        us = round(statistics.median(times), 2)
+        gbs = round(algorithmic_bytes(w) / us / 1e3, 1)
+        metric = "Stage1, headline shape, every KV read an L2 hit (16 shared blocks): headline bytes / time, GB/s"
+        timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
+        dtype = "4-bit K/V, f32 math"
+    elif args.workload == "stage2_b64_s32":
+        import numpy as np
+
+        from tq4_decode import ops, workloads
+
+        w = workloads.qwen3_4b_b64_ctx4096()
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
+        ops.stage1(t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens), t(w.pair_lut), mid)
+        r = stage2_time(dev, flush, timer, w, mid, reps=args.steps)
+        us, gbs = r["us"], r["GBps"]
+        metric = "Stage2 over the headline's mid_o (B64 x 32 heads x 32 splits), fp32 out: GB/s"
+        timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
+        dtype = "f32"
     else:
         r = full_decode_time(dev, flush, timer, reps=args.steps)
         us, gbs = r["us"], r["GBps"]
@@ -449,7 +502,9 @@ def main() -> int:
                     help="also run a 256 MiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--workload", default="stage1",
                     choices=["stage1", "store_decode_b64", "store_prefill_n8192", "full_decode_b256",
-                             "store_k3v4_prefill_n8192", "store_3bit_prefill_n8192", *PRESET_WORKLOADS],
+                             "store_k3v4_prefill_n8192", "store_3bit_prefill_n8192", "stage1_ragged_b64",
+                             "stage1_gqa8_b8_ctx32768", "stage2_b64_s32", "stage1_l2_resident",
+                             *PRESET_WORKLOADS],
                     help="stage1: the headline (default); the others time only that workload "
                          "(--steps cold launches) and print its own JSON line, e.g. for a profile")
     args = ap.parse_args()
