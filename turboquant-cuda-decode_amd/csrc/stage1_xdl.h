@@ -966,6 +966,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         }
     }
     const int lane = threadIdx.x;
+    // Block-table entries of the wave's first tiles, fetched into L2 while seq_lens and the
+    // wave deal are worked out: a guess (the grid's own sequence and run at full length)
+    // that equal lengths make right; the real reads below then hit L2.
+    const int bt_guess =
+        block_table[(int64_t)b * max_blocks + min(wid * ((max_blocks + nw - 1) / nw) + lane, max_blocks - 1)];
     // The pair-LUT rows do not depend on the sequence: they go out first; the K table and the
     // q operands are built once the first tiles' loads are on their way.
     static_assert(!(KF8 && KB3), "one key format");
@@ -1183,6 +1188,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     };
 
     // The first chunk's loads go out before the K table and the q operands are built.
+    asm volatile("" ::"v"(bt_guess));  // (the guess only warms L2; its value is not used)
     open_chunk(0, min(64, total), min(64, total) - 1);
     if constexpr (KB3)
         build_key_table3(ktab, pair_lut, lane);
