@@ -95,9 +95,9 @@ __device__ __forceinline__ float rs_xor32(float a, float c) {
 // sums stay all-positive).  lo is rounded to nearest, so the residual error has no
 // preferred sign and does not build up over a split's tokens.  |x| must stay below 65504.
 __device__ __forceinline__ uint32_t split_f16(float x) {
-    const auto h = __builtin_amdgcn_cvt_pkrtz(x, 0.f);
-    const _Float16 l = (_Float16)(x - (float)h[0]);
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l) << 16);
+    auto h = __builtin_amdgcn_cvt_pkrtz(x, 0.f);
+    h[1] = (__fp16)(x - (float)h[0]);
+    return __builtin_bit_cast(uint32_t, h);
 }
 __device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(half8, uint4{a, b, c, d});
@@ -480,14 +480,15 @@ __device__ __forceinline__ void load_q_rows(float4 (&qx)[8], const float *__rest
     }
 }
 __device__ __forceinline__ void q_operands(half8 (&bq)[8], const float4 (&qx)[8], int n, float scale) {
-    const bool lo = n >= 8;
+    // the lane's part (hi for n < 8, lo for n >= 8) of two split values, packed
+    const uint32_t sel = n >= 8 ? 0x07060302u : 0x05040100u;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         const float4 x = qx[m];
         const uint32_t s0 = split_f16(x.x * scale), s1 = split_f16(x.y * scale);
         const uint32_t s2 = split_f16(x.z * scale), s3 = split_f16(x.w * scale);
-        const uint32_t w0 = lo ? ((s0 >> 16) | (s1 & 0xFFFF0000u)) : ((s0 & 0xFFFFu) | (s1 << 16));
-        const uint32_t w1 = lo ? ((s2 >> 16) | (s3 & 0xFFFF0000u)) : ((s2 & 0xFFFFu) | (s3 << 16));
+        const uint32_t w0 = __builtin_amdgcn_perm(s1, s0, sel);
+        const uint32_t w1 = __builtin_amdgcn_perm(s3, s2, sel);
         bq[m] = as_half8(w0, w0, w1, w1);
     }
 }
@@ -804,6 +805,14 @@ template <int LAYOUT, int G, int WPE> struct SpanCap {
     static_assert(splits >= 1 && floats * 4 <= bytes, "LDS image does not fit");
 };
 
+// LSE of a split, (m + log2 l) * ln 2 with the scores in log2 units.  l >= 1: the running
+// max is only ever set to the score of one of the split's tokens (whose p is then 1), or
+// the caller passes 1 for a split without valid tokens; so the hardware log2 sees a normal
+// number (1 ulp).
+__device__ __forceinline__ float lse_of(float negm, float l) {
+    return (__builtin_amdgcn_logf(l) - negm) * kLn2;
+}
+
 // Rows of one split into image slot j: lane group g ends with heads hA, hA + 1 (see
 // rs_xor32), dims 8n .. 8n + 7; lanes 0 .. G-1 hold the LSE of head n.
 template <int G, class Cap, bool V3 = false>
@@ -846,7 +855,7 @@ __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc
         }
     }
     if (lc.g == 0 && lc.n < G)
-        img[lc.n * Cap::head_floats + j * (kHeadDim + 1) + kHeadDim] = -st.negm * kLn2 + logf(safe_l);
+        img[lc.n * Cap::head_floats + j * (kHeadDim + 1) + kHeadDim] = lse_of(st.negm, safe_l);
 }
 
 // Output element conversion of the fused epilogue (the same roundings as Stage2's).
@@ -891,7 +900,7 @@ __device__ __forceinline__ void emit_output(const State &st, const floatx4 (&acc
         }
     }
     if (lc.g == 0 && lc.n < G)
-        lse[row0 + lc.n] = -st.negm * kLn2 + logf(safe_l);
+        lse[row0 + lc.n] = lse_of(st.negm, safe_l);
 }
 
 // Write image slots 0 .. ns-1 to the rows of splits s0 .. s0+ns-1.  Rows of one head and
@@ -1073,8 +1082,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     };
     // The scheduling barriers keep the loads in program order, which is what lets each
     // wait count only the loads of later tiles.
-    auto issue_kpos = [&](RK &r, uint32_t base_lo, uint32_t base_hi, int j) {
-        const auto rsrc = rsrc_at(base_lo, base_hi, j);
+    // A position's descriptor is built for its K load and kept for its V load, issued one or
+    // two stages later: pos[p & 3] holds position p's (positions j + 4 .. j + 8 around
+    // stage j, and j is a multiple of 4).
+    auto issue_kpos = [&](RK &r, const __amdgpu_buffer_rsrc_t &rsrc) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (KF8 || KB3)
             issue_k(r, rsrc, 0, off);
@@ -1082,8 +1093,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             issue_k<LAYOUT>(r, rsrc, 0, off);
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto issue_vpos = [&](RawV<LAYOUT, TPL> &r, uint32_t base_lo, uint32_t base_hi, int moff_lane, int j) {
-        const auto rsrc = rsrc_at(base_lo, base_hi, j);
+    auto issue_vpos = [&](RawV<LAYOUT, TPL> &r, const __amdgpu_buffer_rsrc_t &rsrc, int moff_lane, int j) {
         const int moff = LAYOUT == 0 ? __builtin_amdgcn_readlane(moff_lane, j & 63) : 0;
         __builtin_amdgcn_sched_barrier(0);
         issue_v<LAYOUT, TPL, KF8, KB3, V3>(r, rsrc, 0, moff, off);
@@ -1151,6 +1161,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     uint32_t base_lo = 0, base_hi = 0;
     RK kr[RING];
     RawV<LAYOUT, TPL> vr[RING];
+    __amdgpu_buffer_rsrc_t pos[RING];
     // Lane tables of chunk [j0, j0 + 64) and the ring's first loads.
     auto open_chunk = [&](int j0, int nchunk, int last) {
         {
@@ -1182,8 +1193,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         }
 #pragma unroll
         for (int k = 0; k < RING; ++k) {
-            issue_kpos(kr[k], base_lo, base_hi, min(j0 + k, last));
-            issue_vpos(vr[k], base_lo, base_hi, moff_lane, min(j0 + k, last));
+            const auto rsrc = rsrc_at(base_lo, base_hi, min(j0 + k, last));
+            issue_kpos(kr[k], rsrc);
+            issue_vpos(vr[k], rsrc, moff_lane, min(j0 + k, last));
         }
     };
 
@@ -1221,16 +1233,18 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                 csq_tot = sum_xor16(sum_xor32(e.csq));
             kn = decode_k<LAYOUT>(kr[1], off);
         }
-        issue_kpos(kr[0], base_lo, base_hi, min(j0 + RING, last));
+        pos[0] = rsrc_at(base_lo, base_hi, min(j0 + RING, last));
+        issue_kpos(kr[0], pos[0]);
         int j = j0;
         do {
 #pragma unroll
             for (int k = 0; k < RING; ++k) {
                 stage(k, vr[(k + RING - 1) % RING], vr[k], kr[(k + 2) % RING], mask_lane, j + k);
-                issue_kpos(kr[(k + 1) % RING], base_lo, base_hi, min(j + k + 1 + RING, last));
+                pos[(k + 1) % RING] = rsrc_at(base_lo, base_hi, min(j + k + 1 + RING, last));
+                issue_kpos(kr[(k + 1) % RING], pos[(k + 1) % RING]);
                 if (k & 1) {
-                    issue_vpos(vr[k - 1], base_lo, base_hi, moff_lane, min(j + k - 1 + RING, last));
-                    issue_vpos(vr[k], base_lo, base_hi, moff_lane, min(j + k + RING, last));
+                    issue_vpos(vr[k - 1], pos[(k + 3) % RING], moff_lane, min(j + k - 1 + RING, last));
+                    issue_vpos(vr[k], pos[k % RING], moff_lane, min(j + k + RING, last));
                     // a split ends after an odd stage (FUSED: the only split ends with the
                     // stream; its rows are written after the loop)
                     if (!FUSED && j + k + 1 == pos_base + cur_stop) {
