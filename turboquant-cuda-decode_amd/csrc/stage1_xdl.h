@@ -72,13 +72,20 @@ __device__ __forceinline__ float sum_xor16(float x) {
     const auto r = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
     return bitsf(r[0]) + bitsf(r[1]);
 }
+// max of two scores, which are never NaN (finite, or -inf for masked tokens): one v_max_f32,
+// without the two quieting v_max that fmaxf adds for operands read across lanes
+__device__ __forceinline__ float max_score(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float max_xor32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(fbits(x), fbits(x), false, false);
-    return fmaxf(bitsf(r[0]), bitsf(r[1]));
+    return max_score(bitsf(r[0]), bitsf(r[1]));
 }
 __device__ __forceinline__ float max_xor16(float x) {
     const auto r = __builtin_amdgcn_permlane16_swap(fbits(x), fbits(x), false, false);
-    return fmaxf(bitsf(r[0]), bitsf(r[1]));
+    return max_score(bitsf(r[0]), bitsf(r[1]));
 }
 // Reduce-scatter over lane halves: lanes 0..31 get a[l] + a[l+32], lanes 32..63 get
 // c[l-32] + c[l].
@@ -657,9 +664,9 @@ __device__ __forceinline__ void lane_dots(const floatx4 &acc, const LaneConst &l
 
 // Max over the lanes of one head (G = 4: lanes n = h mod 4 of all rows; G = 8: n = h mod 8).
 template <int G> __device__ __forceinline__ float head_max(float x) {
-    x = fmaxf(x, dppf<kRor8>(x));
+    x = max_score(x, dppf<kRor8>(x));
     if constexpr (G == 4)
-        x = fmaxf(x, dppf<kRor4>(x));
+        x = max_score(x, dppf<kRor4>(x));
     return max_xor16(max_xor32(x));
 }
 template <int G> __device__ __forceinline__ float head_sum(float x) {
@@ -726,7 +733,7 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
             sn[j] = dot[j] * norm_f[j];
             if (boundary)
                 sn[j] = valid[j] ? sn[j] : -INFINITY;
-            mx = fmaxf(mx, sn[j]);
+            mx = max_score(mx, sn[j]);
         }
         mx = head_max<G>(mx);
         const float negm_new = (mx + st.negm > kRescaleLogX) ? -mx : st.negm;
@@ -813,47 +820,77 @@ __device__ __forceinline__ float lse_of(float negm, float l) {
     return (__builtin_amdgcn_logf(l) - negm) * kLn2;
 }
 
-// Rows of one split into image slot j: lane group g ends with heads hA, hA + 1 (see
-// rs_xor32), dims 8n .. 8n + 7; lanes 0 .. G-1 hold the LSE of head n.
+// Output rows of a finished split held by this lane: heads h0 .. h0 + G/4 - 1, dims 8n ..
+// 8n + 7 each, from the hi and lo halves of the PV sums (lanes l and l ^ 32, summed with
+// rs_xor32), plus the head's softmax sum (safe_l, 1 for an empty split).
+// G = 8: lane group g ends with heads hA = 2 (g >> 1) + 4 (g & 1) and hA + 1 (register
+// elements 0 / 2 and 1 / 3).  G = 4: only lane groups 0 and 2 hold usable rows (rows 0..3
+// hi, 8..11 lo; the A rows 4..7 and 12..15 carry the same heads with their tokens in a
+// rotated slot order, so those sums are discarded).  A v_permlane16_swap of elements 0 and
+// 1 (2 and 3) moves group 0's element 1 (3) into group 1 and group 2's into group 3, and
+// each lane group then finishes one head, g: half the arithmetic of taking two heads in
+// groups 0 and 2 while groups 1 and 3 idle.
+template <int G, bool V3>
+__device__ __forceinline__ void finish_rows(const State &st, const floatx4 (&acc)[8], const LaneConst &lc, int &h0,
+                                            float (&o)[G / 4][8], float &safe_l) {
+    const float lt = head_sum<G>(st.l);
+    const float zt = head_sum<G>(st.z);
+    safe_l = lt > 0.f ? lt : 1.f;
+    // accumulator 2m + 1 holds the whole bytes (even + 16 * odd), or (V3) the odd dim's
+    // codes, in the units of pv_qk; every row holds the totals of head h in lanes n = h (mod G)
+    auto dims = [](float x, float y, float z, float inv, float &even, float &odd) {
+        if constexpr (V3) {
+            even = fmaf(x, kVUnit3, z) * inv;
+            odd = fmaf(y, kVUnit3, z) * inv;
+        } else {
+            even = fmaf(x, kVUnitEven, z) * inv;
+            odd = fmaf(fmaf(y, 16.f, -x), kVUnitOdd, z) * inv;
+        }
+    };
+    if constexpr (G == 4) {
+        h0 = lc.g;
+        // rows 0 and 2 of the result keep element 2k of groups 0 and 2, rows 1 and 3 receive
+        // element 2k + 1 of groups 0 and 2
+        auto head_rows = [](float ek, float ek1) {
+            return bitsf(__builtin_amdgcn_permlane16_swap(fbits(ek), fbits(ek1), false, false)[0]);
+        };
+        const float inv = __builtin_amdgcn_rcpf(__shfl(safe_l, h0, kWave));
+        const float z = __shfl(zt, h0, kWave);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const floatx4 &e = acc[2 * m], &w = acc[2 * m + 1];
+            const float x = rs_xor32(head_rows(e[0], e[1]), head_rows(e[2], e[3]));
+            const float y = rs_xor32(head_rows(w[0], w[1]), head_rows(w[2], w[3]));
+            dims(x, y, z, inv, o[0][2 * m], o[0][2 * m + 1]);
+        }
+    } else {
+        h0 = 2 * (lc.g >> 1) + 4 * (lc.g & 1);
+        const float inv_a = __builtin_amdgcn_rcpf(__shfl(safe_l, h0, kWave));
+        const float inv_b = __builtin_amdgcn_rcpf(__shfl(safe_l, h0 + 1, kWave));
+        const float z_a = __shfl(zt, h0, kWave), z_b = __shfl(zt, h0 + 1, kWave);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
+            const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
+            dims(xa, ya, z_a, inv_a, o[0][2 * m], o[0][2 * m + 1]);
+            dims(xb, yb, z_b, inv_b, o[1][2 * m], o[1][2 * m + 1]);
+        }
+    }
+}
+
+// Rows of one split into image slot j; lanes 0 .. G-1 write the LSE of head n.
 template <int G, class Cap, bool V3 = false>
 __device__ __forceinline__ void stash_split(const State &st, const floatx4 (&acc)[8], const LaneConst &lc,
                                             float *img, int j) {
-    const float lt = head_sum<G>(st.l);
-    const float zt = head_sum<G>(st.z);
-    const float safe_l = lt > 0.f ? lt : 1.f;
-    const int hA = 2 * (lc.g >> 1) + (G == 8 ? 4 * (lc.g & 1) : 0);
-    // every row holds the totals of head h in its lanes n = h (mod G)
-    const float inv_a = __builtin_amdgcn_rcpf(__shfl(safe_l, hA, kWave));
-    const float inv_b = __builtin_amdgcn_rcpf(__shfl(safe_l, hA + 1, kWave));
-    const float z_a = __shfl(zt, hA, kWave), z_b = __shfl(zt, hA + 1, kWave);
-    float oa[8], ob[8];
+    int h0;
+    float o[G / 4][8], safe_l;
+    finish_rows<G, V3>(st, acc, lc, h0, o, safe_l);
+    float *r = img + h0 * Cap::head_floats + j * (kHeadDim + 1) + 8 * lc.n;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        // accumulator 2m + 1 holds the whole bytes (even + 16 * odd), or (V3) the odd dim's
-        // codes, in the units of pv_qk
-        const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
-        const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
-        if constexpr (V3) {
-            oa[2 * m] = fmaf(xa, kVUnit3, z_a) * inv_a;
-            ob[2 * m] = fmaf(xb, kVUnit3, z_b) * inv_b;
-            oa[2 * m + 1] = fmaf(ya, kVUnit3, z_a) * inv_a;
-            ob[2 * m + 1] = fmaf(yb, kVUnit3, z_b) * inv_b;
-        } else {
-            oa[2 * m] = fmaf(xa, kVUnitEven, z_a) * inv_a;
-            ob[2 * m] = fmaf(xb, kVUnitEven, z_b) * inv_b;
-            oa[2 * m + 1] = fmaf(fmaf(ya, 16.f, -xa), kVUnitOdd, z_a) * inv_a;
-            ob[2 * m + 1] = fmaf(fmaf(yb, 16.f, -xb), kVUnitOdd, z_b) * inv_b;
-        }
-    }
-    if (G == 8 || (lc.g & 1) == 0) {
-        float *ra = img + hA * Cap::head_floats + j * (kHeadDim + 1) + 8 * lc.n;
-        float *rb = ra + Cap::head_floats;
+    for (int k = 0; k < G / 4; ++k)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            ra[i] = oa[i];
-            rb[i] = ob[i];
-        }
-    }
+        for (int i = 0; i < 8; ++i)
+            r[k * Cap::head_floats + i] = o[k][i];
     if (lc.g == 0 && lc.n < G)
         img[lc.n * Cap::head_floats + j * (kHeadDim + 1) + kHeadDim] = lse_of(st.negm, safe_l);
 }
@@ -874,31 +911,15 @@ __device__ __forceinline__ void put_out(void *out, int dtype, int64_t i, float v
 template <int G>
 __device__ __forceinline__ void emit_output(const State &st, const floatx4 (&acc)[8], const LaneConst &lc,
                                             void *out, int out_dtype, float *lse, int64_t row0) {
-    const float lt = head_sum<G>(st.l);
-    const float zt = head_sum<G>(st.z);
-    const float safe_l = lt > 0.f ? lt : 1.f;
-    const int hA = 2 * (lc.g >> 1) + (G == 8 ? 4 * (lc.g & 1) : 0);
-    const float inv_a = __builtin_amdgcn_rcpf(__shfl(safe_l, hA, kWave));
-    const float inv_b = __builtin_amdgcn_rcpf(__shfl(safe_l, hA + 1, kWave));
-    const float z_a = __shfl(zt, hA, kWave), z_b = __shfl(zt, hA + 1, kWave);
-    float oa[8], ob[8];
+    int h0;
+    float o[G / 4][8], safe_l;
+    finish_rows<G, false>(st, acc, lc, h0, o, safe_l);
+    const int64_t r = (row0 + h0) * kHeadDim + 8 * lc.n;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const float xa = rs_xor32(acc[2 * m][0], acc[2 * m][2]), ya = rs_xor32(acc[2 * m + 1][0], acc[2 * m + 1][2]);
-        const float xb = rs_xor32(acc[2 * m][1], acc[2 * m][3]), yb = rs_xor32(acc[2 * m + 1][1], acc[2 * m + 1][3]);
-        oa[2 * m] = fmaf(xa, kVUnitEven, z_a) * inv_a;
-        ob[2 * m] = fmaf(xb, kVUnitEven, z_b) * inv_b;
-        oa[2 * m + 1] = fmaf(fmaf(ya, 16.f, -xa), kVUnitOdd, z_a) * inv_a;
-        ob[2 * m + 1] = fmaf(fmaf(yb, 16.f, -xb), kVUnitOdd, z_b) * inv_b;
-    }
-    if (G == 8 || (lc.g & 1) == 0) {
-        const int64_t ra = (row0 + hA) * kHeadDim + 8 * lc.n, rb = ra + kHeadDim;
+    for (int k = 0; k < G / 4; ++k)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            put_out(out, out_dtype, ra + i, oa[i]);
-            put_out(out, out_dtype, rb + i, ob[i]);
-        }
-    }
+        for (int i = 0; i < 8; ++i)
+            put_out(out, out_dtype, r + k * kHeadDim + i, o[k][i]);
     if (lc.g == 0 && lc.n < G)
         lse[row0 + lc.n] = lse_of(st.negm, safe_l);
 }
