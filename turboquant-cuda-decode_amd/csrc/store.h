@@ -33,17 +33,22 @@
 // Reductions over a row's four lanes (n + 16g) use permlane swaps.
 //
 // Bucketize: the workgroup builds a cell table over the midpoints' span (kCells cells of
-// width w, two spare cells each side).  Cell k's window is [y0 + kw - w/64, y0 + (k+1)w +
-// w/64]; its entry holds the one midpoint inside the window (NaN if none), the number of
-// midpoints below the window, and c^2 at those two indices.  A y whose computed cell is k
-// lies inside window k (the computed cell coordinate is off by < 1e-3 cells for |y| < 100;
-// beyond the span the edge cells hold for every y), so count(midpoints <= y) = base +
-// (y >= mid): one LDS read and one compare per element instead of 15.  When some window
-// holds two midpoints (a codebook with a gap under ~w) the kernel counts all 15 instead.
+// width w, about two spare cells each side, centred on y0 + kw with y0 = K w for an integer
+// K).  Cell k's window is [y0 + (k - 1/2)w - w/64, y0 + (k + 1/2)w + w/64]; its entry holds
+// the one midpoint inside the window (NaN if none), the number of midpoints below the
+// window, and c^2 at those two indices.  The cell of y is round(y / w - K), read straight
+// from the bits of fma(y, 1/w, 1.5 * 2^23 - K) (the bias leaves the rounded integer in the
+// low mantissa bits) after a clamp to the table; a y whose computed cell is k lies inside
+// window k (the computed coordinate is off by < 1e-3 cells for |y| <= 1; beyond the span the
+// edge cells hold for every y), so count(midpoints <= y) = base + (y >= mid): one LDS read
+// and one compare per element instead of 15.  When some window holds two midpoints (a
+// codebook with a gap under ~w) the kernel counts all 15 instead.
 //
 // V codes: (v - min) * (1 / scale) is within 2^-18 of the fp32 quotient (v - min) / scale
 // for quotients below 16, so the code (truncation of quotient + 0.5) is the same unless
-// quotient + 0.5 lies within 2^-16 of an integer; such elements take the division.
+// quotient + 0.5 lies within 2^-16 of an integer; such elements take the division (bf16
+// inputs put ~0.2 % of quotients exactly on a half-integer: a per-element branch, since
+// nearly every wave holds one).
 #pragma once
 #include "tq4_device.h"
 
@@ -166,7 +171,7 @@ __device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[
     const float vmax = row_max(hi);
     scale = (vmax - vmin) / (float)kTop;
     scale = scale > 1e-8f ? scale : 1e-8f;
-    const float rs = 1.f / scale;
+    const float rs = __builtin_amdgcn_rcpf(scale);  // 1 ulp: the 2^-18 bound above holds
 #pragma unroll
     for (int q = 0; q < VB; ++q)
         vw[q] = 0u;
@@ -275,11 +280,14 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
         mmax = fmaxf(mmax, mid[i]);
     }
     const float w = (mmax - mmin) / (float)(kCells - 4);
-    const float y0 = mmin - 2.f * w;
-    int cell_ok = 1;
+    // cells centred on y0 + kw, y0 = K w with K an integer: the cell coordinate y / w - K
+    // then needs no fractional offset, and the 1.5 * 2^23 bias rounds it in the same fma
+    const float kcell = floorf((mmin - 2.f * w) / w);
+    const float y0 = kcell * w;
+    int cell_ok = fabsf(kcell) < 0x1p21f;
     if (threadIdx.x < kCells) {
         const int k = threadIdx.x;
-        const float lo = y0 + (float)k * w - w * (1.f / 64), hi = y0 + (float)(k + 1) * w + w * (1.f / 64);
+        const float lo = y0 + ((float)k - 0.5f) * w - w * (1.f / 64), hi = y0 + ((float)k + 0.5f) * w + w * (1.f / 64);
         int base = 0, inside = 0;
         float m_in = __builtin_nanf("");  // compares false with every y
 #pragma unroll
@@ -290,14 +298,15 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
                 m_in = mid[i];
             }
         }
-        cell_ok = inside <= 1 && w > 0.f && w < __builtin_inff();
+        cell_ok = cell_ok && inside <= 1 && w > 0.f && w < __builtin_inff();
         const int up = base < kMids ? base + 1 : kMids;
         // the midpoint is stored x 256, the scale of the rotation's results
         btab[k] = float4{256.f * m_in, __builtin_bit_cast(float, base), c2_at(base), c2_at(up)};
     }
     const bool use_cells = __syncthreads_and(cell_ok) != 0;
-    // cell coordinate (y - y0) / w of y = acc / 256
-    const float inv_w = (1.f / w) * (1.f / 256.f), c0 = -y0 * (1.f / w);
+    // biased cell coordinate y / w - K + 1.5 * 2^23 of y = acc / 256
+    constexpr float kBias = 12582912.f;  // 1.5 * 2^23: the sum's low mantissa bits hold the rounded value
+    const float inv_w = (1.f / w) * (1.f / 256.f), c0 = kBias - kcell;
 
     for (; tile < tiles; tile += stride) {
         const int row = tile * kRows + n;
@@ -358,8 +367,8 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
                 for (int j = 8 * q; j < 8 * q + 8; ++j) {
                     const float a = acc[j / 4][j % 4];
-                    const float t = fminf(fmaxf(fmaf(a, inv_w, c0), 0.f), (float)(kCells - 1));
-                    const float4 e = btab[(int)t];
+                    const float t = fminf(fmaxf(fmaf(a, inv_w, c0), kBias), kBias + (float)(kCells - 1));
+                    const float4 e = btab[__builtin_bit_cast(int, t) - __builtin_bit_cast(int, kBias)];
                     const bool ge = a >= e.x;
                     put_code<KB>(kw, j, (uint32_t)(__builtin_bit_cast(int, e.y) + (ge ? 1 : 0)));
                     csq += ge ? e.w : e.z;
