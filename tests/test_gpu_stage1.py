@@ -175,6 +175,15 @@ def test_wave_deal_gives_a_lone_long_sequence_many_waves(dev):
     assert_parity(run(w, dev, "xdl"), oracle(w))
 
 
+@pytest.mark.parametrize("lens", [[1024] * 32, [1000] * 32])
+def test_equal_lengths_one_full_round(dev, lens):
+    # 8 kv-heads x 32 sequences x 8 waves = 2048 workgroups, one round of the device at two
+    # waves per SIMD, each wave a run of 8 of the 64 splits (1000 tokens: splits of 16 tokens,
+    # the last one short); every split written exactly once
+    w = workloads.small(111, 32, lens, 64)
+    assert_parity(run(w, dev, "xdl"), oracle(w))
+
+
 def test_xdl_ragged_and_gqa8_full_size(dev):
     for w in (workloads.ragged_b64(), workloads.gqa8_b8_ctx32768()):
         assert_parity(run(w, dev, "xdl"), oracle(w))
