@@ -381,11 +381,13 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
 // Waves of one kv-head dealt to the sequences.  The grid gives every kv-head nw * B
 // waves (wave x = wid + nw * b), a number fixed by the shapes alone.  A sequence with live
 // splits gets one wave plus a share of the other nw * B - n_live in proportion to its
-// estimated stream length (prefix rounding: the shares sum to exactly that many), and at
-// most one wave per live split; each wave then takes an equal run of its sequence's live
-// splits.  Every wave of the kv-head computes the same deal from seq_lens, so ragged
-// batches keep the waves about equally busy; equal lengths give every sequence nw waves
-// (taken without the arithmetic).
+// estimated stream length (prefix rounding: the shares sum to at most that many), and at
+// most one wave per live split; each wave then takes a run of its sequence's live splits
+// (k waves over `live` splits: the first live % k runs one split longer).  Every wave of the
+// kv-head computes the same deal from seq_lens, so ragged batches keep the waves about
+// equally busy; equal lengths give every sequence nw waves (taken without the arithmetic);
+// batches of at most 64 sequences also pair heavy runs with light ones on each SIMD
+// (deal_ranked).
 struct Deal {
     int b, wid, nw;  // b < 0: the deal leaves this wave without work
 };
@@ -416,6 +418,69 @@ __device__ __forceinline__ uint32_t wave_scan(uint32_t v) {
 }
 
 // Stream totals stay far below 2^32: a position covers 16 tokens of one kv-head.
+// Lane-wide sum and max (the value of lane 63 after an inclusive scan; max for values >= 0).
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)wave_scan(v), kWave - 1);
+}
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, kWave - 1);
+}
+
+// Batches of at most 64 sequences (one lane each): the waves of the deal, each a run of its
+// sequence's splits (k waves over `live` splits: the first live % k runs one split longer),
+// are ranked by estimated stream positions, heaviest first (ties: by sequence, then run).
+// Grid waves x and x + nw*B/2 share a SIMD when the grid is one round of the device at two
+// waves per SIMD (workgroups i and i + half are dispatched to one SIMD), so they take ranks p
+// and nw*B - 1 - p: a heavy run shares its SIMD with a light one.  The rank-p wave is found
+// by bisection on its load (lane-wide counts of the waves at least that heavy), then by its
+// place among the waves of exactly that load.  Any x -> p bijection keeps the deal exact.
+__device__ Deal deal_ranked(const int32_t *__restrict__ seq_lens, int B, int S, int nw, int x, int lane) {
+    const SeqLoad q = sequence_load(seq_lens, B, S, lane);
+    const uint32_t est_total = wave_sum(q.est);
+    const int n_live = __builtin_popcountll(__ballot(q.live > 0));
+    // spare waves before prefix pre: floor(pre * spare / total) with one fp32 ratio -- monotone
+    // in pre and at most `spare` at the total, the same on every wave (all the deal needs)
+    const float ratio = est_total > 0 ? (float)((int64_t)nw * B - n_live) / (float)est_total : 0.f;
+    auto cut = [&](uint32_t pre) { return (int)floorf((float)pre * ratio); };
+    const uint32_t est_out = wave_scan(q.est);
+    const int k = q.live > 0 ? min(1 + cut(est_out) - cut(est_out - q.est), q.live) : 0;
+    const int per = q.live > 0 ? (int)(q.est / (uint32_t)q.live) : 0;  // positions per split
+    const int qd = k > 0 ? q.live / k : 0, r = k > 0 ? q.live % k : 0;
+    const uint32_t l_hi = (uint32_t)((qd + 1) * per), l_lo = (uint32_t)(qd * per);
+    const int n_hi = r, n_lo = k - r;  // runs of qd + 1 and of qd splits
+    const int T = nw * B;
+    const int p = (T % 2 == 0 && x >= T / 2) ? 3 * T / 2 - 1 - x : x;
+    if ((uint32_t)p >= wave_sum((uint32_t)k))
+        return Deal{-1, 0, 0};
+    auto count_ge = [&](uint32_t t) {
+        return wave_sum((uint32_t)((n_hi > 0 && l_hi >= t ? n_hi : 0) + (n_lo > 0 && l_lo >= t ? n_lo : 0)));
+    };
+    // the load of rank p: the largest t with more than p waves at least that heavy
+    uint32_t lo = 0, hi = wave_max(n_hi > 0 ? l_hi : l_lo) + 1;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (count_ge(mid) > (uint32_t)p)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    const int idx = p - (int)count_ge(lo + 1);
+    const bool hi_in = n_hi > 0 && l_hi == lo;
+    const int in_b = hi_in ? n_hi : (n_lo > 0 && l_lo == lo ? n_lo : 0);
+    const int incl = (int)wave_scan((uint32_t)in_b), excl = incl - in_b;
+    const uint64_t hit = __ballot(in_b > 0 && idx >= excl && idx < incl);
+    const int sq = __builtin_ctzll(hit);
+    const int j0 = idx - __builtin_amdgcn_readlane(excl, sq);
+    const int j = __builtin_amdgcn_readlane(hi_in ? 1 : 0, sq) ? j0 : __builtin_amdgcn_readlane(r, sq) + j0;
+    return Deal{sq, j, __builtin_amdgcn_readlane(k, sq)};
+}
+
 __device__ Deal deal_waves(const int32_t *__restrict__ seq_lens, int B, int S, int nw, int x, int lane) {
     // equal lengths: every sequence keeps its nw waves, as the deal would give them
     const int len0 = seq_lens[0];
@@ -426,6 +491,8 @@ __device__ Deal deal_waves(const int32_t *__restrict__ seq_lens, int B, int S, i
     }
     if (equal)
         return Deal{x / nw, x % nw, nw};
+    if (B <= kWave)
+        return deal_ranked(seq_lens, B, S, nw, x, lane);
     const SeqLoad first = sequence_load(seq_lens, B, S, lane);
     uint32_t est_total = 0;
     int n_live = 0;
@@ -1024,9 +1091,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     // split partition: L = ceil(len / S); live splits are those with s * L < len
     const int split_len = (seq_len + num_splits - 1) / num_splits;
     const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
-    // wave x of the W waves of this (sequence, kv-head) takes live splits [x * live / W, (x + 1) * live / W)
-    const int s_lo = (int)((int64_t)wid * live / run_waves);
-    const int s_hi = (int)((int64_t)(wid + 1) * live / run_waves);
+    // run x of the W runs of this (sequence, kv-head): live splits from x q + min(x, r), q + 1 of
+    // them for x < r and q after (q = live / W, r = live % W)
+    const int run_q = live / run_waves, run_r = live % run_waves;
+    const int s_lo = wid * run_q + min(wid, run_r);
+    const int s_hi = s_lo + run_q + (wid < run_r ? 1 : 0);
     if constexpr (FUSED) {
         if (live == 0) {
             // an empty sequence: what Stage2 writes for it (0 / 0 and ln 0)
