@@ -18,7 +18,7 @@ def _mid_on_gpu(w, dev):
 
 
 @pytest.mark.parametrize("lens,splits", [([1, 3, 17, 100, 257, 999], 32), ([4096, 4095], 32),
-                                         ([5000, 70], 64), ([64], 1)])
+                                         ([5000, 70], 64), ([64], 1), ([9999, 5000, 33], 100)])
 def test_stage2_matches_oracle_and_skips_empty_splits(dev, lens, splits):
     w = workloads.small(201, len(lens), lens, splits)
     mid = _mid_on_gpu(w, dev)  # empty splits hold NaN: merging one would poison the output

@@ -11,8 +11,13 @@ template <> __device__ __forceinline__ _Float16 from_float<_Float16>(float x) { 
 
 template <typename T> __device__ __forceinline__ float to_float(T x) { return (float)x; }
 
-// One wave per (q-head, sequence); lane owns dims 2*lane, 2*lane+1.  Pass 1 takes the
-// max LSE over the non-empty splits, pass 2 accumulates exp(lse - max)-weighted rows.
+// One wave per (q-head, sequence); lane owns dims 2*lane, 2*lane+1.  The non-empty splits
+// are merged 32 at a time in one pass: lane i reads split i's LSE while every lane reads its
+// two dims of all 32 rows (buffer loads at any 4-byte offset: the 516-byte rows are not
+// 8-byte aligned), so a wave has its whole share of mid_o in flight at once; then the
+// weights exp(lse_s - max) are broadcast lane by lane.  A later chunk (more than 32 splits)
+// rescales what came before to its own max.
+constexpr int kMergeRows = 32;
 template <typename OutT>
 __global__ __launch_bounds__(kWave) void stage2_kernel(const float *__restrict__ mid_o,
                                                       const int32_t *__restrict__ seq_lens,
@@ -26,22 +31,41 @@ __global__ __launch_bounds__(kWave) void stage2_kernel(const float *__restrict__
     const int split_len = (seq_len + num_splits - 1) / num_splits;
     // splits [0, live) are the non-empty ones: split s is non-empty iff s * len < seq_len
     const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
-    const float *base = mid_o + ((int64_t)b * num_q_heads + h) * num_splits * (kHeadDim + 1);
+    constexpr int kRow = (kHeadDim + 1) * 4;  // bytes per split row
+    const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(mid_o + ((int64_t)b * num_q_heads + h) * num_splits * (kHeadDim + 1)), 0, 0x7FFFFFFF,
+        0x00020000);
 
-    float mx = -INFINITY;
-    for (int s = lane; s < live; s += kWave)
-        mx = fmaxf(mx, base[(int64_t)s * (kHeadDim + 1) + kHeadDim]);
-    mx = wave_max(mx);
-
-    float a0 = 0.f, a1 = 0.f, wsum = 0.f;
-    // unrolled so that several split rows are loaded at a time
-#pragma unroll 8
-    for (int s = 0; s < live; ++s) {
-        const float *row = base + (int64_t)s * (kHeadDim + 1);
-        const float w = expf(row[kHeadDim] - mx);
-        a0 += w * row[2 * lane];
-        a1 += w * row[2 * lane + 1];
-        wsum += w;
+    float mx = -INFINITY, a0 = 0.f, a1 = 0.f, wsum = 0.f;
+    for (int s0 = 0; s0 < live; s0 += kMergeRows) {
+        const int n = min(kMergeRows, live - s0);
+        const float l = lane < n ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                  rows, (s0 + lane) * kRow + kHeadDim * 4, 0, 0))
+                                 : -INFINITY;
+        // rows past the chunk re-read its last row (a cache hit); their weight is 0
+        float v0[kMergeRows], v1[kMergeRows];
+#pragma unroll
+        for (int i = 0; i < kMergeRows; ++i) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rows, (s0 + min(i, n - 1)) * kRow + 8 * lane, 0, 0);
+            // (elements copied out first: a bit cast applied to an element of the vector
+            // in place reads element 0)
+            const uint32_t x0 = v[0], x1 = v[1];
+            v0[i] = __builtin_bit_cast(float, x0);
+            v1[i] = __builtin_bit_cast(float, x1);
+        }
+        const float m_new = fmaxf(mx, wave_max(l));
+        const float scale = expf(mx - m_new);  // 0 for the first chunk (mx = -inf)
+        const float w = expf(l - m_new);       // 0 on lanes past the chunk
+        a0 *= scale;
+        a1 *= scale;
+        wsum = wsum * scale + wave_sum(w);
+#pragma unroll
+        for (int i = 0; i < kMergeRows; ++i) {
+            const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+            a0 = fmaf(wi, v0[i], a0);
+            a1 = fmaf(wi, v1[i], a1);
+        }
+        mx = m_new;
     }
     const float inv = 1.f / wsum;
     OutT *o = out + ((int64_t)b * num_q_heads + h) * kHeadDim;
