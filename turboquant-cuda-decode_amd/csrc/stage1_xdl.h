@@ -1061,6 +1061,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             wid = pair % nw;
             b = pair / nw;
         }
+    } else {
+        // The two waves of a SIMD are workgroups i and i + half the grid (one round at 2
+        // waves per SIMD), and with the plain map both would serve the same kv-head.  Odd
+        // kv-heads read ~7 % slower from HBM (their records are the upper halves of 256-byte
+        // stretches), so SIMDs holding two of them would end last: the second half of the
+        // grid takes kv-head h ^ 1 instead, and every SIMD runs one even and one odd kv-head.
+        // The kv-heads of one (sequence, wave) pair still start together and read in step.
+        if ((gridDim.x & 1) == 0 && 2 * (wid + nw * b) >= nw * (int)gridDim.z)
+            kvh ^= 1;
     }
     const int lane = threadIdx.x;
     // Block-table entries of the wave's first tiles, fetched into L2 while seq_lens and the
