@@ -1061,16 +1061,16 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             wid = pair % nw;
             b = pair / nw;
         }
-    } else {
-        // The two waves of a SIMD are workgroups i and i + half the grid (one round at 2
-        // waves per SIMD), and with the plain map both would serve the same kv-head.  Odd
-        // kv-heads read ~7 % slower from HBM (their records are the upper halves of 256-byte
-        // stretches), so SIMDs holding two of them would end last: the second half of the
-        // grid takes kv-head h ^ 1 instead, and every SIMD runs one even and one odd kv-head.
-        // The kv-heads of one (sequence, wave) pair still start together and read in step.
-        if ((gridDim.x & 1) == 0 && 2 * (wid + nw * b) >= nw * (int)gridDim.z)
-            kvh ^= 1;
     }
+    // The two waves of a SIMD are workgroups i and i + half the grid (one round at 2 waves
+    // per SIMD), and with either map above both would serve the same kv-head.  kv-heads read
+    // HBM at different speeds by where their records sit in the cache rows (4-bit SoA: the
+    // odd ones, upper halves of 256-byte stretches, ~7 % slower), so SIMDs holding two slow
+    // ones would end last: the second half of the grid takes kv-head h ^ 1 instead, and
+    // every SIMD runs one even and one odd kv-head.  The kv-heads of one (sequence, wave)
+    // pair still start together (and share an XCD where the map above puts them on one).
+    if ((gridDim.x & 1) == 0 && 2 * (wid + nw * b) >= nw * (int)gridDim.z)
+        kvh ^= 1;
     const int lane = threadIdx.x;
     // Block-table entries of the wave's first tiles, fetched into L2 while seq_lens and the
     // wave deal are worked out: a guess (the grid's own sequence and run at full length)
