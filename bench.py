@@ -127,11 +127,14 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
-def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4)):
+def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4), slots_mode="random"):
     """Cache writer (SoA, bf16 K/V, norm correction) cold, kernel duration: one decode step
     (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  ``bits``: key / value bits
     (4/4: tq4_store; 3/4 and 3/3: tq4_store_preset).  Bytes per (token, kv-head): 2 x 256
-    read + the slot written, plus 4 of slot mapping per token."""
+    read + the slot written, plus 4 of slot mapping per token.  ``slots_mode``: "random"
+    (the tokens scattered over the block pool: each block's metadata fields get their tokens
+    from different workgroups) or "contiguous" (token t in slot t: blocks filled in order,
+    as a prefill of one sequence fills them)."""
     import numpy as np
     import torch
 
@@ -152,7 +155,10 @@ def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4)):
         val = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
         n_blocks = (n_tok + 15) // 16 + 4
         cache = torch.zeros(n_blocks, 16, 8, slot, dtype=torch.uint8, device=dev)
-        slots = torch.randperm(n_blocks * 16, device=dev)[:n_tok].to(torch.int32)
+        if slots_mode == "contiguous":
+            slots = torch.arange(n_tok, device=dev, dtype=torch.int32)
+        else:
+            slots = torch.randperm(n_blocks * 16, device=dev)[:n_tok].to(torch.int32)
         times = []
         for i in range(reps + 3):
             flush.sum()
@@ -415,10 +421,10 @@ def side_workload(args, dev) -> int:
         for tag, b in (("k3v4_", (3, 4)), ("3bit_", (3, 3))):
             if size.startswith(tag):
                 size, bits = size[len(tag):], b
-        r = store_times(dev, flush, timer, reps=args.steps, only=size, bits=bits)
+        r = store_times(dev, flush, timer, reps=args.steps, only=size, bits=bits, slots_mode=args.slots)
         us, gbs = r[f"{size}_us"], r[f"{size}_GBps"]
         entry = "tq4_store" if bits == (4, 4) else f"tq4_store_preset {bits[0]}/{bits[1]}"
-        metric = f"cache writer ({entry}, SoA, bf16 K/V, 8 kv-heads) {size}: GB/s"
+        metric = f"cache writer ({entry}, SoA, bf16 K/V, 8 kv-heads, {args.slots} slots) {size}: GB/s"
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = "bf16 in, f32 math"
     elif args.workload in ("stage1_ragged_b64", "stage1_gqa8_b8_ctx32768"):
@@ -495,6 +501,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layout", default="soa", choices=["soa", "aos"])
+    ap.add_argument("--slots", default="random", choices=["random", "contiguous"],
+                    help="writer workloads: token slots scattered over the pool, or in order")
     ap.add_argument("--kernel", default="auto", choices=["auto", "simple", "xdl"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-variants", action="store_true")
