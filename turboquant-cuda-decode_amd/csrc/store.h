@@ -55,7 +55,9 @@
 namespace tq4 {
 namespace store {
 
-constexpr int kWaves = 8;           // waves per workgroup
+constexpr int kWaves = 8;           // waves per workgroup (launches of up to kSmallTiles tiles: 4)
+constexpr int kSmallWaves = 4;
+constexpr int kSmallTiles = 1024;   // 4-wave workgroups up to this many tiles: at most one per CU
 constexpr int kRows = 16;           // rows per wave step
 constexpr int kMaxGroups = 512;     // two resident workgroups per CU (LDS), 4 waves per SIMD
 constexpr int kCells = 128;         // bucketize table cells
@@ -191,8 +193,12 @@ __device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[
 // 3 / 4 (turboquant_k3v4_nc) and 3 / 3 (turboquant_3bit_nc) pack 8 codes in 3 bytes
 // (reference/soa_store.py:319-337, :47-83): SoA record 16 KB + 16 VB bytes, AoS slot
 // K | norm | V | scale | zero padded to even, written with 2-byte stores.
-template <int LAYOUT, class T, int KB = 4, int VB = 4>
-__global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4))) void store_kernel(
+// W: waves per workgroup.  8 for large launches (two workgroups per CU share the CU's LDS,
+// 4 waves per SIMD); 4 for launches of at most kSmallTiles tiles (a decode step's few
+// rows), so that the waves spread over twice the CUs at one wave per SIMD: a wave's tile
+// arithmetic then has its SIMD to itself, at the price of staging twice the PiT share.
+template <int LAYOUT, class T, int KB = 4, int VB = 4, int W = kWaves>
+__global__ __launch_bounds__(kWave *W) __attribute__((amdgpu_waves_per_eu(W == kWaves ? 4 : 1))) void store_kernel(
     const T *__restrict__ key, const T *__restrict__ value, const int32_t *__restrict__ slot_mapping,
     const float *__restrict__ pit, const float *__restrict__ midpoints, const float *__restrict__ centroids,
     uint8_t *__restrict__ cache, int rows, int num_kv_heads, int block_size, int64_t block_stride,
@@ -205,8 +211,8 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int n = lane & 15, g = lane >> 4;
     const int tiles = (rows + kRows - 1) / kRows;
-    const int stride = gridDim.x * kWaves;
-    int tile = blockIdx.x * kWaves + wave;
+    const int stride = gridDim.x * W;
+    int tile = blockIdx.x * W + wave;
 
     // Every workgroup reads PiT, the midpoints and the centroids (L2 hits after the first
     // workgroup): their loads go out ahead of the first tile's K and V.  Those reads, across
@@ -228,11 +234,11 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
     }
     // thread (c, k8): 16 * PiT[8k8 .. 8k8+7][c] (coalesced over c) -> one 16-byte LDS write
     // into each part
-    constexpr int kStage = kHeadDim * (kHeadDim / 8) / (kWave * kWaves);
+    constexpr int kStage = kHeadDim * (kHeadDim / 8) / (kWave * W);
     float pw[kStage][8];
 #pragma unroll
     for (int it = 0; it < kStage; ++it) {
-        const int i = threadIdx.x + it * kWave * kWaves;
+        const int i = threadIdx.x + it * kWave * W;
         const int c = i % kHeadDim, k8 = i / kHeadDim;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -251,7 +257,7 @@ __global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(4
 
 #pragma unroll
     for (int it = 0; it < kStage; ++it) {
-        const int i = threadIdx.x + it * kWave * kWaves;
+        const int i = threadIdx.x + it * kWave * W;
         const int c = i % kHeadDim, k8 = i / kHeadDim;
         half8 h, l;
 #pragma unroll

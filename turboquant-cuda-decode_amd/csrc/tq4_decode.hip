@@ -343,13 +343,20 @@ int launch_store(const void *key, const void *value, int dtype, const int32_t *s
                  const float *rot_t, const float *midpoints, const float *centroids, uint8_t *kv_cache,
                  int rows, int Hk, int block_size, int64_t cache_block_stride, const CacheGeom &geom,
                  int norm_correction, hipStream_t st, const char *what) {
-    const int per_group = tq4::store::kRows * tq4::store::kWaves;
-    const dim3 grid(std::min<int64_t>((rows + per_group - 1) / per_group, tq4::store::kMaxGroups));
-#define TQ4_STORE_LAUNCH(L, T)                                                                            \
-    launch(&tq4::store::store_kernel<L, T, KB, VB>, grid, dim3(tq4::kWave * tq4::store::kWaves), st,      \
-           static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t, midpoints,      \
-           centroids, kv_cache, rows, Hk, block_size, cache_block_stride, geom.pos, geom.head,              \
-           norm_correction)
+    // few tiles: 4-wave workgroups, one per CU at most (see store_kernel)
+    const int64_t tiles = ((int64_t)rows + tq4::store::kRows - 1) / tq4::store::kRows;
+    const bool small = tiles <= tq4::store::kSmallTiles;
+    const int waves = small ? tq4::store::kSmallWaves : tq4::store::kWaves;
+    const dim3 grid(std::min<int64_t>((tiles + waves - 1) / waves, tq4::store::kMaxGroups));
+#define TQ4_STORE_LAUNCH(L, T)                                                                             \
+    (small ? launch(&tq4::store::store_kernel<L, T, KB, VB, tq4::store::kSmallWaves>, grid,               \
+                    dim3(tq4::kWave * tq4::store::kSmallWaves), st, static_cast<const T *>(key),            \
+                    static_cast<const T *>(value), slot_mapping, rot_t, midpoints, centroids, kv_cache,     \
+                    rows, Hk, block_size, cache_block_stride, geom.pos, geom.head, norm_correction)         \
+           : launch(&tq4::store::store_kernel<L, T, KB, VB>, grid, dim3(tq4::kWave * tq4::store::kWaves),   \
+                    st, static_cast<const T *>(key), static_cast<const T *>(value), slot_mapping, rot_t,    \
+                    midpoints, centroids, kv_cache, rows, Hk, block_size, cache_block_stride, geom.pos,     \
+                    geom.head, norm_correction))
     switch (dtype * 2 + geom.kl) {
     case TQ4_F32 * 2 + 0: TQ4_STORE_LAUNCH(0, float); break;
     case TQ4_F32 * 2 + 1: TQ4_STORE_LAUNCH(1, float); break;
