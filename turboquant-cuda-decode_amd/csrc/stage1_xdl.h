@@ -1072,11 +1072,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     if ((gridDim.x & 1) == 0 && 2 * (wid + nw * b) >= nw * (int)gridDim.z)
         kvh ^= 1;
     const int lane = threadIdx.x;
-    // Block-table entries of the wave's first tiles, fetched into L2 while seq_lens and the
-    // wave deal are worked out: a guess (the grid's own sequence and run at full length)
-    // that equal lengths make right; the real reads below then hit L2.
-    const int bt_guess =
-        block_table[(int64_t)b * max_blocks + min(wid * ((max_blocks + nw - 1) / nw) + lane, max_blocks - 1)];
+    // Block-table entries of the wave's first tiles, loaded while seq_lens and the wave deal
+    // are worked out: a guess (the grid's own sequence and run at full length) that equal
+    // lengths make right.  When the first chunk's entries turn out to be exactly these, the
+    // registers serve it and the block-table read leaves the path to the first KV loads;
+    // otherwise the guess has warmed L2 for the real reads.
+    const int guess_b = b, guess_first = wid * ((max_blocks + nw - 1) / nw);
+    const int bt_guess = block_table[(int64_t)b * max_blocks + min(guess_first + lane, max_blocks - 1)];
     // The pair-LUT rows do not depend on the sequence: they go out first; the K table and the
     // q operands are built once the first tiles' loads are on their way.
     static_assert(!(KF8 && KB3), "one key format");
@@ -1280,7 +1282,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             }
         }
         {
-            const int blk = bt[(16 * tile_lane) >> block_size_log2];
+            const int bidx = (16 * tile_lane) >> block_size_log2;
+            const bool guessed = j0 == 0 && b == guess_b &&
+                                 __ballot(bidx != min(guess_first + lane, max_blocks - 1)) == 0;
+            const int blk = guessed ? bt_guess : bt[bidx];
             const int toff = (16 * tile_lane) & (block_size - 1);
             // the piece's first record: token toff of kv-head 0 (AoS: at toff * slot_pos)
             const int piece = LAYOUT == 0 ? toff * num_kv_heads * rec : toff * slot_pos;
@@ -1299,7 +1304,6 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     };
 
     // The first chunk's loads go out before the K table and the q operands are built.
-    asm volatile("" ::"v"(bt_guess));  // (the guess only warms L2; its value is not used)
     open_chunk(0, min(64, total), min(64, total) - 1);
     if constexpr (KB3)
         build_key_table3(ktab, pair_lut, lane);
