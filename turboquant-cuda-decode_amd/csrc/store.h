@@ -160,6 +160,15 @@ __device__ __forceinline__ void store16_a2(uint8_t *p, uint4 v) {
 // word j / 8).  The product with the reciprocal is within 2^-18 of the fp32 quotient for
 // quotients below 16, so the code only differs when quotient + 0.5 lies within 2^-16 of an
 // integer: those elements take the division.
+//
+// 4-bit codes take a shorter path.  q = v * rs + (-min * rs) in one fma differs from the real
+// quotient R = (v - min) / scale by at most 15 * 2^-23 (rs, 1 ulp) + |min * rs| * 2^-24 (the
+// rounded addend) + 2^-20 (the fma's rounding), and the fp32 quotient + 0.5 from R + 0.5 by
+// at most 2^-19 + 2^-20: together under e = 2^-17 + |min * rs| * 2^-24.  Where q lies further
+// than 2e from every half-integer, round-to-nearest(q) = trunc(R + 0.5) = the code, and
+// v_cvt_pk_u8_f32 (round to nearest even, saturating to 0..255, NaN to 0) rounds q and packs
+// it into a byte in one instruction; even and odd elements fill two words of bytes that one
+// shift-or merges into nibbles.  The other elements take the division as above.
 template <int VB = 4>
 __device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[VB], float &scale, float &vmin) {
     constexpr int kTop = (1 << VB) - 1;
@@ -174,6 +183,27 @@ __device__ __forceinline__ void quantize_v(const float (&x)[32], uint32_t (&vw)[
     scale = (vmax - vmin) / (float)kTop;
     scale = scale > 1e-8f ? scale : 1e-8f;
     const float rs = __builtin_amdgcn_rcpf(scale);  // 1 ulp: the 2^-18 bound above holds
+    if constexpr (VB == 4) {
+        const float nb = -vmin * rs;
+        // |q - rint(q)| below lim: q is more than 2e from the half-integers (NaN: no branch,
+        // code 0 as the division's path gives)
+        const float lim = 0.5f - (0x1p-16f + fabsf(nb) * 0x1p-22f);
+        uint32_t ev[4] = {0u, 0u, 0u, 0u}, od[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            float q = fmaf(x[j], rs, nb);
+            if (fabsf(q - rintf(q)) >= lim) {  // near a code boundary: the division
+                asm volatile("");
+                q = fminf(floorf((x[j] - vmin) / scale + 0.5f), (float)kTop);
+            }
+            uint32_t &w = (j & 1) ? od[j / 8] : ev[j / 8];
+            w = __builtin_amdgcn_cvt_pk_u8_f32(q, (j % 8) / 2, w);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            vw[i] = ev[i] | (od[i] << 4);
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < VB; ++q)
         vw[q] = 0u;
