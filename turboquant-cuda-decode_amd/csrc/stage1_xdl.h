@@ -118,8 +118,8 @@ __device__ __forceinline__ float half_at(uint32_t w, int hi) {
 
 // K-code table indexed by one packed byte (low nibble = even dim, high nibble = odd dim):
 // entry e = ((c_hi[lo], c_hi[hi]), (c_lo[lo], c_lo[hi])) as two f16 pairs, read with one
-// ds_read_b64 straight into half of a QK^T operand; AoS adds a second table of
-// c[lo]^2 + c[hi]^2 (fp32) for the norm correction.
+// ds_read_b64 straight into half of a QK^T operand; the AoS norm correction sums
+// c[lo]^2 + c[hi]^2 from the same entries (f16 dot products into fp32, lookup_tile).
 template <int LAYOUT> struct KTable {
     static constexpr int words = 512;
 };
