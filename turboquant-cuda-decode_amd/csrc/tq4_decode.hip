@@ -242,10 +242,11 @@ template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
     case 1: launch_simple<LAYOUT, 1>(a, st); break;
     case 2: launch_simple<LAYOUT, 2>(a, st); break;
     case 4: launch_simple<LAYOUT, 4>(a, st); break;
+    case 6: launch_simple<LAYOUT, 6>(a, st); break;
     case 8: launch_simple<LAYOUT, 8>(a, st); break;
     case 16: launch_simple<LAYOUT, 16>(a, st); break;
     default:
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: GQA group %d unsupported (1, 2, 4, 8, 16)",
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: GQA group %d unsupported (1, 2, 4, 6, 8, 16)",
                     a.Hq / a.Hk);
     }
     return launch_status("stage1_simple");
