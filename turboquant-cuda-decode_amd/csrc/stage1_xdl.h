@@ -40,6 +40,7 @@
 // is written out as one contiguous run per head (see SpanCap).
 #pragma once
 #include <type_traits>
+#include "stage2.h"
 #include "tq4_device.h"
 
 namespace tq4 {
@@ -146,6 +147,21 @@ __device__ __forceinline__ void build_key_table(uint32_t *tbl, const LutRows &v,
         const int e = lane + kWave * i;
         const float c_lo = v.r[i].x, c_hi = v.r[i].y;
         const uint32_t p_lo = split_f16(c_lo), p_hi = split_f16(c_hi);
+        tbl[2 * e] = (p_lo & 0xFFFFu) | (p_hi << 16);
+        tbl[2 * e + 1] = (p_lo >> 16) | (p_hi & 0xFFFF0000u);
+    }
+}
+
+// The rows i = w (mod nw) of the table (entries lane + 64 i), for a table that nw waves of a
+// workgroup build together.
+template <int LAYOUT>
+__device__ __forceinline__ void build_key_table_rows(uint32_t *tbl, const LutRows &v, int lane, int w, int nw) {
+#pragma unroll
+    for (int i = 0; i < 256 / kWave; ++i) {
+        if (i % nw != w)
+            continue;
+        const int e = lane + kWave * i;
+        const uint32_t p_lo = split_f16(v.r[i].x), p_hi = split_f16(v.r[i].y);
         tbl[2 * e] = (p_lo & 0xFFFFu) | (p_hi << 16);
         tbl[2 * e + 1] = (p_lo >> 16) | (p_hi & 0xFFFF0000u);
     }
@@ -975,29 +991,32 @@ __device__ __forceinline__ void put_out(void *out, int dtype, int64_t i, float v
 // One split per sequence: with a single live split Stage2's merge is the identity (weight
 // exp(0) = 1, sum 1), so the wave writes the final output rows and LSE itself -- the same
 // values Stage2 would write, without the mid_o round trip.
+// Heads nh .. G-1 of the wave are padding (a GQA group that is not a multiple of G).
 template <int G>
 __device__ __forceinline__ void emit_output(const State &st, const floatx4 (&acc)[8], const LaneConst &lc,
-                                            void *out, int out_dtype, float *lse, int64_t row0) {
+                                            void *out, int out_dtype, float *lse, int64_t row0, int nh) {
     int h0;
     float o[G / 4][8], safe_l;
     finish_rows<G, false>(st, acc, lc, h0, o, safe_l);
     const int64_t r = (row0 + h0) * kHeadDim + 8 * lc.n;
 #pragma unroll
     for (int k = 0; k < G / 4; ++k)
+        if (h0 + k < nh)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            put_out(out, out_dtype, r + k * kHeadDim + i, o[k][i]);
-    if (lc.g == 0 && lc.n < G)
+            for (int i = 0; i < 8; ++i)
+                put_out(out, out_dtype, r + k * kHeadDim + i, o[k][i]);
+    if (lc.g == 0 && lc.n < nh)
         lse[row0 + lc.n] = lse_of(st.negm, safe_l);
 }
 
-// Write image slots 0 .. ns-1 to the rows of splits s0 .. s0+ns-1.  Rows of one head and
-// consecutive splits are consecutive in mid_o [B, Hq, S, D + 1], so head h's slots are one
-// run of ns * 129 floats.  One wave: its LDS accesses complete in program order, so only
-// the compiler must keep the image reads after the writes.
+// Write image slots 0 .. ns-1 to the rows of splits s0 .. s0+ns-1 (heads 0 .. nh-1; the
+// rest are padding).  Rows of one head and consecutive splits are consecutive in mid_o
+// [B, Hq, S, D + 1], so head h's slots are one run of ns * 129 floats.  One wave: its LDS
+// accesses complete in program order, so only the compiler must keep the image reads after
+// the writes.
 template <int G, class Cap>
 __device__ __forceinline__ void flush_splits(const float *img, float *__restrict__ mid_o, int64_t row0,
-                                             int num_splits, int s0, int ns, int lane) {
+                                             int num_splits, int s0, int ns, int lane, int nh) {
     asm volatile("" ::: "memory");
     const int64_t head_bytes = (int64_t)num_splits * (kHeadDim + 1) * 4;
     float *base = mid_o + (row0 * num_splits + s0) * (kHeadDim + 1);
@@ -1006,6 +1025,8 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
     const int chunks = run >> 2;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
+        if (h >= nh)
+            break;
         const float *src = img + h * Cap::head_floats;
         for (int c = lane; c < chunks; c += kWave) {
             const float4 v = *reinterpret_cast<const float4 *>(src + 4 * c);
@@ -1020,6 +1041,107 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
     asm volatile("" ::: "memory");
 }
 
+// ---- Query rotation inside the one-split kernel (ROT) --------------------------------
+// A workgroup holds the nvh waves of one sequence (nvh = its kv-heads times the parts of
+// their GQA groups, a divisor of 8: at most two waves per SIMD of one CU).  Together they
+// compute the sequence's rotated queries q_rot = query @ rot_t into LDS with the operands
+// and the MFMA order of rotate_mfma_kernel, so the rows are bit-identical to that launch's:
+// each query row scaled by the power of two that puts its largest |x| in [2^14, 2^15) (exact
+// in f16 for fp16 / bf16 queries), rot_t as f16 hi + lo parts, D[rows 4g .. 4g+3][col n] of
+// output column tile c per row tile.  Wave w takes the column tiles c = w, w + nvh, ..., so it
+// reads 8 KB of rot_t per tile (one column slab), not the whole 64 KB.
+constexpr int kRotGroupWaves = 8;
+constexpr int kQRowFloats = kHeadDim + 4;  // LDS row of a rotated query (rows 16 bytes apart in bank)
+
+// Query elements of the lane for every row tile of the sequence: row 16t + n (rows past Hq
+// repeat the last one and are not stored), elements 32kb + 8g .. +7 -- the A operand of
+// rotate_mfma_kernel.  Hq <= 8 G, so G / 2 row tiles.
+template <int G> struct RotRows {
+    uint4 raw[G / 2][4];
+};
+template <typename InT, int G>
+__device__ __forceinline__ void rot_load_rows(RotRows<G> &a, const InT *__restrict__ query, int64_t row_base,
+                                              int hq, int n, int g) {
+#pragma unroll
+    for (int t = 0; t < G / 2; ++t) {
+        const int row = min(16 * t + n, hq - 1);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+            a.raw[t][kb] = *reinterpret_cast<const uint4 *>(query + (row_base + row) * kHeadDim + 32 * kb + 8 * g);
+    }
+}
+// rot_t[32kb + 8g + j][16c + n]: the lane's B operand of column tile c (fp32, split later).
+struct RotCols {
+    float v[4][8];
+};
+__device__ __forceinline__ void rot_load_cols(RotCols &b, const float *__restrict__ rot_t, int c, int n, int g) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            b.v[kb][j] = rot_t[(32 * kb + 8 * g + j) * kHeadDim + 16 * c + n];
+}
+// Scaled f16 A operands of every row tile and the scale exponents of the D rows each lane
+// receives (row 4g + i of tile t).
+template <typename InT, int G>
+__device__ __forceinline__ void rot_a_operands(const RotRows<G> &a, half8 (&ah)[G / 2][4], int (&e_out)[G / 2][4],
+                                               int g) {
+    typedef InT in8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+    for (int t = 0; t < G / 2; ++t) {
+        float amax = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const in8 p = __builtin_bit_cast(in8, a.raw[t][kb]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                amax = fmaxf(amax, fabsf(to_float<InT>(p[j])));
+        }
+        amax = rot_row_max(amax);
+        const int e = (amax > 0.f && amax < __builtin_inff()) ? 15 - __builtin_amdgcn_frexp_expf(amax) : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            e_out[t][i] = __shfl(e, 4 * g + i, kWave);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const in8 p = __builtin_bit_cast(in8, a.raw[t][kb]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                ah[t][kb][j] = (_Float16)__builtin_ldexpf(to_float<InT>(p[j]), e);
+        }
+    }
+}
+// Column tile c of every row tile into the LDS rows qbuf [Hq][kQRowFloats].
+template <int G>
+__device__ __forceinline__ void rot_column_tile(const half8 (&ah)[G / 2][4], const int (&e_out)[G / 2][4],
+                                                const RotCols &b, float *qbuf, int c, int hq, int n, int g) {
+    half8 bh[4], bl[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            bh[kb][j] = (_Float16)b.v[kb][j];
+            bl[kb][j] = (_Float16)(b.v[kb][j] - (float)bh[kb][j]);
+        }
+#pragma unroll
+    for (int t = 0; t < G / 2; ++t) {
+        if (16 * t >= hq)
+            break;
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            acc = mfma(ah[t][kb], bh[kb], acc);
+            acc = mfma(ah[t][kb], bl[kb], acc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * t + 4 * g + i;
+            if (row < hq)
+                qbuf[row * kQRowFloats + 16 * c + n] = __builtin_ldexpf(acc[i], -e_out[t][i]);
+        }
+    }
+}
+
 // One wave handles a run of consecutive live splits of one (sequence, kv-head).  Their
 // tiles form one stream: split s contributes n_s tiles padded to a multiple of 4 stream
 // positions (padding positions re-read the split's last tile and mask every token), so
@@ -1027,25 +1149,50 @@ __device__ __forceinline__ void flush_splits(const float *img, float *__restrict
 // stage the wave puts its rows into the LDS image (flushed to mid_o when full and after
 // the wave's last split) and restarts the softmax state and the accumulators.
 //
-// FUSED (launched with one split per sequence and one wave per (sequence, kv-head)): the
+// GQA groups: a wave serves G (4 or 8) q-heads of one kv-head.  A group of more than G
+// heads is served by parts of G heads (ceil(group / G) waves per kv-head, each reading the
+// kv-head's tiles), and a group that is not a multiple of G leaves the last part's heads
+// nh .. G-1 as padding (zero queries, never written).  Grid x runs over the (part, kv-head)
+// pairs, vh = part * Hk + kv-head.
+//
+// FUSED (launched with one split per sequence and one wave per (sequence, kv-head part)): the
 // wave writes the final output rows (out, out_dtype) and LSE instead of mid_o rows.
+// ROT (with FUSED; 1: bf16 queries, 2: fp16): a workgroup is the nvh waves of one sequence
+// (grid (B)), which rotate the query themselves (q_rot is not read: `query`, `rot_t`, and
+// pair_lut holds the 16 centroids).
 // KF8: the FP8-key preset (K one E4M3 byte per dim, no norm, the query not rotated).
 // KB3: the 3-bit-key / 4-bit-value preset (pair_lut then holds the 8 centroids).
-template <int LAYOUT, int G, int WPE, bool FUSED, bool KF8 = false, bool KB3 = false, bool V3 = false>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void stage1_xdl_kernel(
+template <int LAYOUT, int G, int WPE, bool FUSED, bool KF8 = false, bool KB3 = false, bool V3 = false, int ROT = 0>
+__global__ __launch_bounds__(ROT ? kWave * kRotGroupWaves : kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void stage1_xdl_kernel(
     const float *__restrict__ q_rot, const uint8_t *__restrict__ cache,
     const int32_t *__restrict__ block_table, const int32_t *__restrict__ seq_lens,
     const float *__restrict__ pair_lut, float *__restrict__ mid_o, const float *__restrict__ sinks,
     void *__restrict__ out, int out_dtype, float *__restrict__ lse,
     int num_q_heads, int num_kv_heads, int block_size_log2, int max_blocks, int64_t block_stride,
-    int slot_pos, int slot_head, int num_splits, float score_scale_log2) {
-    static_assert(G == 4 || G == 8, "GQA group 4 or 8");
+    int slot_pos, int slot_head, int num_splits, float score_scale_log2,
+    const void *__restrict__ query, const float *__restrict__ rot_t) {
+    static_assert(G == 4 || G == 8, "4 or 8 q-heads per wave");
+    static_assert(ROT == 0 || (FUSED && !KF8 && !KB3), "the query rotation runs in the one-split 4-bit kernel");
+    using QueryT = std::conditional_t<ROT == 1, __bf16, _Float16>;
     constexpr int TPL = G / 4;
     constexpr int RING = 4;
     const int block_size = 1 << block_size_log2;
-    int kvh = blockIdx.x, wid = blockIdx.y, b = blockIdx.z;
-    const int nw = gridDim.y;
-    if constexpr (LAYOUT == 1 || KF8 || KB3) {
+    int vh, wid, b;
+    if constexpr (ROT) {
+        // wave w of the sequence's workgroup; with 8 waves (2 per SIMD: waves w and w + 4 share
+        // one) SIMD s gets parts 2s and 2s + 1, one even and one odd kv-head (see below)
+        const int w = threadIdx.x / kWave;
+        vh = blockDim.x == kWave * 8 ? 2 * (w & 3) + (w >> 2) : w;
+        wid = 0;
+        b = blockIdx.x;
+    } else {
+        vh = blockIdx.x;
+        wid = blockIdx.y;
+        b = blockIdx.z;
+    }
+    const int nw = ROT ? 1 : gridDim.y;
+    if constexpr (!ROT && (LAYOUT == 1 || KF8 || KB3)) {
         // Workgroups are dealt to the XCDs round-robin by linear id (8 on gfx950), so with
         // the plain map kv-head h runs on XCD h.  An AoS slot (or a preset's SoA record of
         // 192, 112 or 96 bytes) of kv-head h shares 128-byte lines with those of h - 1 and h + 1: the kv-heads of one (sequence, wave)
@@ -1057,7 +1204,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
             const int lin = blockIdx.x + hk * (blockIdx.y + gridDim.y * blockIdx.z);
             const int r = lin / kXcds;
             const int pair = lin % kXcds + kXcds * (r / hk);
-            kvh = r % hk;
+            vh = r % hk;
             wid = pair % nw;
             b = pair / nw;
         }
@@ -1069,9 +1216,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     // ones would end last: the second half of the grid takes kv-head h ^ 1 instead, and
     // every SIMD runs one even and one odd kv-head.  The kv-heads of one (sequence, wave)
     // pair still start together (and share an XCD where the map above puts them on one).
-    if ((gridDim.x & 1) == 0 && 2 * (wid + nw * b) >= nw * (int)gridDim.z)
-        kvh ^= 1;
-    const int lane = threadIdx.x;
+    if (!ROT && (gridDim.x & 1) == 0 && 2 * (wid + nw * b) >= nw * (int)gridDim.z)
+        vh ^= 1;
+    const int lane = threadIdx.x % kWave;
+    const int group = num_q_heads / num_kv_heads;
+    const int kvh = vh % num_kv_heads, part = vh / num_kv_heads;
+    const int hb = kvh * group + part * G;       // the wave's first q-head
+    const int nh = min(G, group - part * G);     // its real q-heads (the rest are padding)
+    const int hl = min((lane & 15) & (G - 1), nh - 1);  // the lane's q-head (padding: a real one's)
     // Block-table entries of the wave's first tiles, loaded while seq_lens and the wave deal
     // are worked out: a guess (the grid's own sequence and run at full length) that equal
     // lengths make right.  When the first chunk's entries turn out to be exactly these, the
@@ -1085,8 +1237,16 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     static_assert(!V3 || (KB3 && !FUSED), "3-bit values come with 3-bit keys, not fused");
     using RK = std::conditional_t<KF8, RawK8, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>;
     LutRows lut_rows{};
-    if constexpr (!KF8 && !KB3)
+    if constexpr (ROT) {
+        // from the centroids themselves: entry e = (c[e & 15], c[e >> 4]), the pair-LUT row
+#pragma unroll
+        for (int i = 0; i < 256 / kWave; ++i) {
+            const int e = lane + kWave * i;
+            lut_rows.r[i] = float2{pair_lut[e & 15], pair_lut[e >> 4]};
+        }
+    } else if constexpr (!KF8 && !KB3) {
         lut_rows = load_lut_rows(pair_lut, lane);
+    }
     int run_waves = nw;  // waves sharing this wave's sequence and kv-head
     if constexpr (!FUSED) {
         const Deal d = deal_waves(seq_lens, gridDim.z, num_splits, nw, wid + nw * b, lane);
@@ -1097,7 +1257,17 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         run_waves = d.nw;
     }
     float4 q_rows[8];
-    load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + kvh * G + ((lane & 15) & (G - 1)), lane >> 4, KF8);
+    RotRows<G> rot_rows;
+    RotCols rot_cols;
+    const int nvh = ROT ? (int)(blockDim.x / kWave) : 1;
+    if constexpr (ROT) {
+        // the rotation's loads go out before the first KV loads (their wait then skips those)
+        rot_load_rows<QueryT, G>(rot_rows, static_cast<const QueryT *>(query), (int64_t)b * num_q_heads,
+                                 num_q_heads, lane & 15, lane >> 4);
+        rot_load_cols(rot_cols, rot_t, threadIdx.x / kWave, lane & 15, lane >> 4);
+    } else {
+        load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + hb + hl, lane >> 4, KF8);
+    }
     const int seq_len = seq_lens[b];
     // split partition: L = ceil(len / S); live splits are those with s * L < len
     const int split_len = (seq_len + num_splits - 1) / num_splits;
@@ -1109,12 +1279,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
     const int s_hi = s_lo + run_q + (wid < run_r ? 1 : 0);
     if constexpr (FUSED) {
         if (live == 0) {
-            // an empty sequence: what Stage2 writes for it (0 / 0 and ln 0)
-            const int64_t r0 = ((int64_t)b * num_q_heads + kvh * G) * kHeadDim;
-            for (int i = lane; i < G * kHeadDim; i += kWave)
+            // an empty sequence: what Stage2 writes for it (0 / 0 and ln 0); with ROT every
+            // wave of the workgroup returns here (one sequence), before its barrier
+            const int64_t r0 = ((int64_t)b * num_q_heads + hb) * kHeadDim;
+            for (int i = lane; i < nh * kHeadDim; i += kWave)
                 put_out(out, out_dtype, r0 + i, __builtin_nanf(""));
-            if (lane < G)
-                lse[(int64_t)b * num_q_heads + kvh * G + lane] = -__builtin_inff();
+            if (lane < nh)
+                lse[(int64_t)b * num_q_heads + hb + lane] = -__builtin_inff();
             return;
         }
     }
@@ -1131,14 +1302,15 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
 
     __shared__ uint32_t ktab[KTable<LAYOUT>::words];
     using Cap = SpanCap<LAYOUT, G, WPE>;
-    __shared__ __align__(16) float img[Cap::floats];
+    __shared__ __align__(16) float img[FUSED ? 4 : Cap::floats];  // FUSED writes no mid_o rows
+    __shared__ __align__(16) float qbuf[ROT ? kRotGroupWaves * G * kQRowFloats : 4];
     half8 bq[8];
 
     State st{__FLT_MAX__, 0.f, 0.f, 1.f};
     if (sinks && s_lo == 0) {
         // split 0 starts from the head's sink logit: max = sink, sum = 1 (one lane per head,
         // lane h, holds it; the sums are totalled over the lanes n = h (mod G))
-        st.negm = -sinks[(int64_t)kvh * G + (lc.n & (G - 1))] * kLog2e;
+        st.negm = -sinks[(int64_t)hb + hl] * kLog2e;
         st.l = lane < G ? 1.f : 0.f;
     }
     floatx4 acc[8];
@@ -1164,7 +1336,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         lane_offsets<LAYOUT, G, KF8, KB3, V3>(lc.n, lc.g, kvh, num_kv_heads, block_size, slot_pos, slot_head);
     const int32_t *bt = block_table + (int64_t)b * max_blocks;
     const int tok0 = 4 * lc.g + TPL * (lc.n / G);  // the lane's first softmax token
-    const int64_t row0 = (int64_t)b * num_q_heads + kvh * G;
+    const int64_t row0 = (int64_t)b * num_q_heads + hb;
     const int rec = record_bytes<LAYOUT, KF8, KB3, V3>();
 
     int cur = s_lo;
@@ -1305,10 +1477,39 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
 
     // The first chunk's loads go out before the K table and the q operands are built.
     open_chunk(0, min(64, total), min(64, total) - 1);
-    if constexpr (KB3)
-        build_key_table3(ktab, pair_lut, lane);
-    else if constexpr (!KF8)
-        build_key_table<LAYOUT>(ktab, lut_rows, lane);
+    if constexpr (ROT) {
+        // the sequence's rotated queries into qbuf (column tiles w, w + nvh, ... of this wave)
+        half8 ah[G / 2][4];
+        int e_out[G / 2][4];
+        rot_a_operands<QueryT, G>(rot_rows, ah, e_out, lc.g);
+        const int w = threadIdx.x / kWave;
+        rot_column_tile<G>(ah, e_out, rot_cols, qbuf, w, num_q_heads, lc.n, lc.g);
+        for (int c = w + nvh; c < kHeadDim / 16; c += nvh) {
+            rot_load_cols(rot_cols, rot_t, c, lc.n, lc.g);
+            rot_column_tile<G>(ah, e_out, rot_cols, qbuf, c, num_q_heads, lc.n, lc.g);
+        }
+        // the shared K table: wave w builds rows i = w (mod nvh) of it
+        build_key_table_rows<LAYOUT>(ktab, lut_rows, lane, w, nvh);
+        // LDS writes done, then the workgroup barrier (the KV loads stay in flight: no
+        // vmcnt wait, unlike __syncthreads)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+            q_rows[m] = *reinterpret_cast<const float4 *>(qbuf + (hb + hl) * kQRowFloats + 32 * lc.g + 4 * m);
+        if (hl != ((lane & 15) & (G - 1)))
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+                q_rows[m] = float4{0.f, 0.f, 0.f, 0.f};
+    } else {
+        if (hl != ((lane & 15) & (G - 1)))  // padding head: a zero query
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+                q_rows[m] = float4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (KB3)
+            build_key_table3(ktab, pair_lut, lane);
+        else if constexpr (!KF8)
+            build_key_table<LAYOUT>(ktab, lut_rows, lane);
+    }
     q_operands(bq, q_rows, lc.n, score_scale_log2);
     // one wave: its LDS writes complete before its later LDS reads; only the compiler must
     // keep the table lookups after the build
@@ -1353,7 +1554,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
                     if (!FUSED && j + k + 1 == pos_base + cur_stop) {
                         stash_split<G, Cap, V3>(st, acc, lc, img, cur - img_s0);
                         if (cur + 1 == s_hi || cur + 1 - img_s0 == Cap::splits) {
-                            flush_splits<G, Cap>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane);
+                            flush_splits<G, Cap>(img, mid_o, row0, num_splits, img_s0, cur + 1 - img_s0, lane, nh);
                             img_s0 = cur + 1;
                         }
                         // fresh softmax state; the next split's first max change owes nothing
@@ -1373,7 +1574,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE, WPE)
         } while (j <= last);
     }
     if constexpr (FUSED)
-        emit_output<G>(st, acc, lc, out, out_dtype, lse, row0);
+        emit_output<G>(st, acc, lc, out, out_dtype, lse, row0, nh);
 }
 
 }  // namespace xdl

@@ -90,6 +90,11 @@ struct Stage1Args {
     // > 0: the key_bits / value_bits preset on the VALU kernel; lut holds the 2^key_bits
     // centroids (not the pair LUT)
     int key_bits = 0, value_bits = 4;
+    // set (with out): the one-split kernel rotates this query itself (TQ4_BF16 / TQ4_F16 rows
+    // [B, Hq, D]) with rot_t, and lut holds the 16 centroids instead of the pair LUT
+    const void *query = nullptr;
+    int query_dtype = TQ4_F32;
+    const float *rot_t = nullptr;
     // filled by check_stage1: kernel layout (0 SoA, 1 AoS) and the AoS slot strides
     int kl = 0, slot_pos = 0, slot_head = 0;
 };
@@ -169,7 +174,15 @@ template <int LAYOUT, int G> void launch_simple(const Stage1Args &a, hipStream_t
                        a.max_blocks, a.stride, a.slot_pos, a.slot_head, a.S, a.scale * tq4::kLog2e);
 }
 
-// Waves per (sequence, kv-head) for the 16x16x32 kernel; wave x takes splits
+// q-heads per wave of the 16x16x32 kernel (4 for GQA groups up to 4, else 8) and the waves
+// (parts) each kv-head's group takes.
+int xdl_heads(const Stage1Args &a) { return a.Hq / a.Hk <= 4 ? 4 : 8; }
+int xdl_parts(const Stage1Args &a) {
+    const int g = a.Hq / a.Hk, h = xdl_heads(a);
+    return (g + h - 1) / h;
+}
+
+// Waves per (sequence, kv-head part) for the 16x16x32 kernel; wave x takes splits
 // [x * S / W, (x + 1) * S / W).  Consecutive splits in one wave share one load
 // pipeline, which removes per-split start-up latency; W is chosen so the grid fills
 // whole rounds of the waves the GPU holds at the kernel's occupancy.  `slots` caches that
@@ -194,7 +207,7 @@ int waves_per_sequence(const Stage1Args &a, const void *kernel, std::atomic<int>
             held = 256 * 4 * 2;
         slots.store(held, std::memory_order_relaxed);
     }
-    const int64_t pairs = (int64_t)a.Hk * a.B;
+    const int64_t pairs = (int64_t)a.Hk * xdl_parts(a) * a.B;
     // smallest number of whole rounds that gives every pair at least one wave
     const int64_t rounds = (pairs + held - 1) / held;
     int64_t w = rounds * held / pairs;
@@ -218,13 +231,30 @@ template <int LAYOUT, int G, bool KF8 = false, bool KB3 = false, bool V3 = false
     return waves_per_sequence(a, reinterpret_cast<const void *>(kernel), slots);
 }
 
+// The one-split kernel that rotates the query itself: one workgroup per sequence holding its
+// Hk * parts waves, which must divide 8 (two waves per SIMD of one CU).
+bool rot_applies(const Stage1Args &a) {
+    const int nvh = a.Hk * xdl_parts(a);
+    return (a.query_dtype == TQ4_BF16 || a.query_dtype == TQ4_F16) && 8 % nvh == 0;
+}
+
 template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st) {
     constexpr int wpe = xdl_waves_per_simd<LAYOUT, G>();
     const bool kb3 = a.key_bits == 3, v3 = a.value_bits == 3;
+    const int nvh = a.Hk * xdl_parts(a);
+    if (a.query) {  // one split per sequence, the rotation inside (Stage2 fused)
+        const auto kernel = a.query_dtype == TQ4_BF16
+                                ? &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, true, false, false, false, 1>
+                                : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, true, false, false, false, 2>;
+        launch(kernel, dim3(a.B), dim3(tq4::kWave * nvh), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
+               a.mid_o, a.sinks, a.out, a.out_dtype, a.lse, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks,
+               a.stride, a.slot_pos, a.slot_head, a.S, a.scale * tq4::kLog2e, a.query, a.rot_t);
+        return;
+    }
     const int waves = a.key_fp8 ? xdl_waves<LAYOUT, G, true>(a)
                       : kb3     ? (v3 ? xdl_waves<LAYOUT, G, false, true, true>(a) : xdl_waves<LAYOUT, G, false, true>(a))
                                 : xdl_waves<LAYOUT, G>(a);
-    const dim3 grid(a.Hk, waves, a.B);
+    const dim3 grid(nvh, waves, a.B);
     auto kernel = a.out ? &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, true>
                         : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false>;
     if (a.key_fp8)  // never fused: the FP8-key decode runs Stage2 itself
@@ -234,7 +264,7 @@ template <int LAYOUT, int G> void launch_xdl(const Stage1Args &a, hipStream_t st
                     : &tq4::xdl::stage1_xdl_kernel<LAYOUT, G, wpe, false, false, true>;
     launch(kernel, grid, dim3(tq4::kWave), st, a.q_rot, a.cache, a.bt, a.seq_lens, a.lut,
            a.mid_o, a.sinks, a.out, a.out_dtype, a.lse, a.Hq, a.Hk, log2_int(a.bs), a.max_blocks,
-           a.stride, a.slot_pos, a.slot_head, a.S, a.scale * tq4::kLog2e);
+           a.stride, a.slot_pos, a.slot_head, a.S, a.scale * tq4::kLog2e, nullptr, nullptr);
 }
 
 template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
@@ -252,17 +282,20 @@ template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
     return launch_status("stage1_simple");
 }
 
+// GQA groups of 3 and more: groups up to 4 on 4-head waves, larger ones in parts of 8 heads
+// (6: one part with two padding heads; 16: two parts).  Groups of 1 and 2 would leave most of
+// the matrix-core columns idle and run on the VALU kernel.
 bool mfma_applies(const Stage1Args &a) {
     const int g = a.Hq / a.Hk;
     const bool pow2 = a.bs >= 16 && (a.bs & (a.bs - 1)) == 0;
-    return (g == 4 || g == 8) && pow2 && a.stride % 16 == 0;
+    return g >= 3 && pow2 && a.stride % 16 == 0;
 }
 
 template <int LAYOUT> int dispatch_xdl(const Stage1Args &a, hipStream_t st) {
     if (!mfma_applies(a))
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: XDL kernel needs GQA group 4 or 8, a "
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: XDL kernel needs a GQA group of 3 or more, a "
                                        "power-of-two block_size >= 16 and a 16-byte block stride");
-    if (a.Hq / a.Hk == 4)
+    if (xdl_heads(a) == 4)
         launch_xdl<LAYOUT, 4>(a, st);
     else
         launch_xdl<LAYOUT, 8>(a, st);
@@ -274,7 +307,7 @@ template <int LAYOUT> int dispatch_xdl(const Stage1Args &a, hipStream_t st) {
 int auto_xdl_waves(const Stage1Args &a) {
     if (!mfma_applies(a))
         return 0;
-    const bool g4 = a.Hq / a.Hk == 4;
+    const bool g4 = xdl_heads(a) == 4;
     if (a.kl == 0)
         return g4 ? xdl_waves<0, 4>(a) : xdl_waves<0, 8>(a);
     return g4 ? xdl_waves<1, 4>(a) : xdl_waves<1, 8>(a);
@@ -552,22 +585,18 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
                     float attn_scale, const float *sinks, tq4_stream_t stream) {
     if (!centroids || !pair_lut_ws)
         return fail(TQ4_E_INVALID, "tq4_full_decode: null pointer argument");
-    // one launch rotates the query and writes the pair LUT
-    int rc = rotate_query(query, query_dtype, rot_t, q_rot_ws, B * Hq, D, centroids, pair_lut_ws,
-                          reinterpret_cast<hipStream_t>(stream));
-    if (rc)
-        return rc;
-    // When the Stage1 kernel gives each (sequence, kv-head) one wave anyway, that wave runs
-    // the whole sequence as one split: the same attention (up to rounding), without writing
-    // and re-reading num_kv_splits rows per head (with sinks too: the sink enters split 0,
-    // the only split then).
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    // When the Stage1 kernel gives each (sequence, kv-head part) one wave anyway, that wave
+    // runs the whole sequence as one split: the same attention (up to rounding), without
+    // writing and re-reading num_kv_splits rows per head (with sinks too: the sink enters
+    // split 0, the only split then).  Stage2's merge of one split is the identity, so the
+    // Stage1 kernel writes the output rows and LSE itself (mid_o is not written then).
     Stage1Args a{q_rot_ws, kv_cache, block_table, seq_lens, pair_lut_ws, mid_o, B, Hq, Hk, D,
                  block_size, max_blocks_per_seq, cache_block_stride, num_kv_splits, layout,
                  attn_scale, sinks};
-    // With one split per sequence Stage2's merge is the identity, so the Stage1 kernel
-    // writes the output rows and LSE itself (mid_o is not written then).
+    a.query_dtype = query_dtype;
     if (check_stage1(a) == TQ4_OK && auto_xdl_waves(a) == 1) {
-        if (!out || !lse)
+        if (!out || !lse || !query || !rot_t)
             return fail(TQ4_E_INVALID, "tq4_full_decode: null pointer argument");
         if (out_dtype != TQ4_F32 && out_dtype != TQ4_BF16 && out_dtype != TQ4_F16)
             return fail(TQ4_E_INVALID, "tq4_full_decode: out_dtype must be 0 (f32), 1 (bf16) or 2 (f16)");
@@ -575,9 +604,22 @@ int tq4_full_decode(const void *query, int query_dtype, const float *rot_t,
         a.out = out;
         a.out_dtype = out_dtype;
         a.lse = lse;
-        return run_stage1(a, TQ4_KERNEL_XDL, reinterpret_cast<hipStream_t>(stream));
+        if (rot_applies(a) && aligned(query, 16)) {
+            // one launch: the workgroup of each sequence rotates its query into LDS (the
+            // workspaces q_rot_ws and pair_lut_ws are not written)
+            a.query = query;
+            a.rot_t = rot_t;
+            a.lut = centroids;
+            return run_stage1(a, TQ4_KERNEL_XDL, st);
+        }
+        const int rc = rotate_query(query, query_dtype, rot_t, q_rot_ws, B * Hq, D, centroids, pair_lut_ws, st);
+        return rc ? rc : run_stage1(a, TQ4_KERNEL_XDL, st);
     }
-    rc = run_stage1(a, TQ4_KERNEL_AUTO, reinterpret_cast<hipStream_t>(stream));
+    // one launch rotates the query and writes the pair LUT
+    int rc = rotate_query(query, query_dtype, rot_t, q_rot_ws, B * Hq, D, centroids, pair_lut_ws, st);
+    if (rc)
+        return rc;
+    rc = run_stage1(a, TQ4_KERNEL_AUTO, st);
     if (rc)
         return rc;
     return tq4_stage2(mid_o, seq_lens, out, out_dtype, lse, B, Hq, D, a.S, stream);
@@ -608,7 +650,10 @@ int tq4_full_decode_noalloc(const void *query, int query_dtype, const float *rot
     float *mid_o = reinterpret_cast<float *>(bytes + lut_bytes + q_bytes);
     Stage1Args a{q_rot, kv_cache, block_table, seq_lens, lut, mid_o, B, Hq, Hk, D, block_size,
                  max_blocks_per_seq, cache_block_stride, num_kv_splits, layout, attn_scale, sinks};
-    const bool one_split = check_stage1(a) == TQ4_OK && auto_xdl_waves(a) == 1;
+    rc = check_stage1(a);  // invalid arguments report their own error, not a workspace size
+    if (rc)
+        return rc;
+    const bool one_split = auto_xdl_waves(a) == 1;
     const size_t mid_bytes = one_split ? 0 : (size_t)B * Hq * num_kv_splits * (D + 1) * sizeof(float);
     const size_t need = lut_bytes + q_bytes + mid_bytes;
     if (need > kScratchBytes)
