@@ -59,12 +59,31 @@ def test_ragged_with_empty_and_partial_splits(dev, kernel, layout):
     assert_parity(run(w, dev, kernel, layout, cache), oracle(w, layout, cache))
 
 
-@pytest.mark.parametrize("kernel,group", [("simple", 1), ("simple", 2), ("simple", 4),
-                                          ("simple", 8), ("simple", 16), ("xdl", 4), ("xdl", 8)])
+@pytest.mark.parametrize("kernel,group", [("simple", 1), ("simple", 2), ("simple", 4), ("simple", 6),
+                                          ("simple", 8), ("simple", 16), ("xdl", 3), ("xdl", 4),
+                                          ("xdl", 6), ("xdl", 8), ("xdl", 12), ("xdl", 16)])
 def test_gqa_groups(dev, kernel, group):
+    """The matrix-core kernel serves a group in waves of 4 (groups up to 4) or 8 q-heads:
+    3 and 6 leave padding heads in their wave, 12 and 16 take two waves per kv-head."""
     hk = 4
     w = workloads.small(102, 3, [77, 300, 1024], 7, num_q_heads=hk * group, num_kv_heads=hk)
     assert_parity(run(w, dev, kernel), oracle(w))
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("group", [6, 16])
+def test_gqa_6_and_16_on_the_mfma_kernel(dev, layout, group):
+    """GQA 6 and 16 (the backend's gfx950 groups besides 8) at 8 kv-heads: many splits per
+    wave, an empty and a one-token sequence; auto runs the 16x16x32 kernel."""
+    hk = 8
+    w = workloads.small(103 + group, 5, [4096, 0, 1, 333, 2049], 32, num_q_heads=hk * group,
+                        num_kv_heads=hk)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, hk) if layout == "aos" else None
+    ref = oracle(w, layout, cache)
+    xdl = run(w, dev, "xdl", layout, cache)
+    assert_parity(xdl, ref, 1e-5)  # fp32-grade on this data, inside the 1e-4 bar
+    assert np.array_equal(run(w, dev, "auto", layout, cache), xdl, equal_nan=True)
+    assert_parity(run(w, dev, "simple", layout, cache), ref)
 
 
 @pytest.mark.parametrize("kernel", ["simple", "xdl"])
@@ -226,7 +245,7 @@ def test_reference_call_shapes(qwen, dev):
 
 @pytest.mark.parametrize("kernel", ["xdl", "simple"])
 @pytest.mark.parametrize("layout", ["soa", "aos"])
-@pytest.mark.parametrize("group", [4, 8])
+@pytest.mark.parametrize("group", [4, 6, 8, 16])
 def test_sinks(dev, kernel, layout, group):
     """Per-head sink logits enter split 0's softmax (max = sink, sum = 1)."""
     hk = 4
