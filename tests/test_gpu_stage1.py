@@ -121,6 +121,48 @@ def test_large_scores_rescale_path(dev):
     assert_parity(run(w, dev, "simple"), oracle(w))
 
 
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("group", [4, 8])
+def test_query_rows_beyond_the_f16_range(dev, layout, group):
+    """q rows whose |q * attn_scale * log2 e| reaches 1e5 - 5e5 (past the f16 range of the
+    matrix-core operands; they are scaled by a power of two first) next to rows just inside
+    it and ordinary rows.  Scores that large make a (split, head) row ill-conditioned when
+    its top two tokens lie within a few units: a relative rounding of 2^-22 of the scores
+    then moves the output by more than 1e-4 in any fp32 kernel.  So the float64 oracle is
+    run twice, the second time with q scaled by 1 + 2^-20, and the rows that move by less
+    than 1e-5 (at least 90 % of them) are held to 1e-4 on the outputs and 1e-4 + 2^-20
+    relative on the LSE; every row must be finite."""
+    from oracle import stage1 as ostage
+
+    hk = 4
+    w = workloads.small(109 + group, 3, [700, 64, 1500], 4, num_q_heads=hk * group, num_kv_heads=hk)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, hk) if layout == "aos" else w.kv_cache
+    q = w.q_rot.copy()
+    q[0, 1] *= 2e5
+    q[1, :] *= 3e4
+    q[2, group] *= 1e6
+    w.q_rot = q
+    got = run(w, dev, "xdl", layout, None if layout == "soa" else cache)
+
+    def f64(qq):
+        return ostage.stage1(qq, cache, w.block_table, w.seq_lens, w.centroids, 4, num_kv_heads=hk,
+                             is_aos=layout == "aos")
+
+    ref = f64(q)
+    nudged = f64(q.astype(np.float64) * (1 + 2.0 ** -20))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    live = ~np.isnan(ref[..., 0])
+    assert np.isfinite(got[live]).all()
+    well = live & (np.abs(nudged[..., :128] - ref[..., :128]).max(-1) < 1e-5)
+    assert well.sum() >= 0.9 * live.sum()
+    err_o = np.abs(got[..., :128] - ref[..., :128])[well].max()
+    lse_g, lse_r = got[..., 128][well], ref[..., 128][well]
+    print(f"{well.sum()} of {live.sum()} rows well-conditioned; outputs max-abs {err_o:.3e}, "
+          f"LSE up to {np.abs(lse_r).max():.3e}")
+    assert err_o <= 1e-4
+    assert np.all(np.abs(lse_g - lse_r) <= 1e-4 + 2.0 ** -20 * np.abs(lse_r))
+
+
 @pytest.fixture(scope="module")
 def qwen():
     w = workloads.qwen3_4b_b64_ctx4096()

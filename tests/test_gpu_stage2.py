@@ -130,6 +130,31 @@ def test_full_decode_reference_ext_shape(dev):
     assert np.abs(lse.cpu().numpy() - fl).max() <= 1e-4
 
 
+def test_ext_stage2_without_seq_lens_merges_every_split(dev):
+    """``ext.tq4_cuda_v7_stage2(mid_o, output, lse)`` has the reference V7 signature, without
+    seq_lens (``cuda/tq4_cuda_v7.cu:56-76``), and merges every split of every row, as that
+    kernel does: its precondition is that Stage1 wrote all of them, i.e. every length gives
+    S non-empty splits (``ceil(len / ceil(len / S)) == S``: 77 tokens over 32 splits of 3
+    leave 6 empty).  Lengths that are multiples of 32 over 32 splits: the result equals the
+    merge of the non-empty splits (the seq_lens form) bit for bit, and the oracle."""
+    w = workloads.small(206, 4, [4096, 2016, 32, 96], 32)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    mid = torch.full((4, 32, 32, 129), float("nan"), device=dev)
+    ops.ext.tq4_cuda_v7_stage1(t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens),
+                               t(w.centroids), mid)
+    out, lse = torch.empty(4, 32, 128, device=dev), torch.empty(4, 32, device=dev)
+    ops.ext.tq4_cuda_v7_stage2(mid, out, lse)
+    out2, lse2 = torch.empty_like(out), torch.empty_like(lse)
+    ops.ext.tq4_cuda_v7_stage2(mid, out2, lse2, t(w.seq_lens))
+    torch.cuda.synchronize()
+    assert not torch.isnan(mid).any(), "every split was written"
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    fo, fl = ostage.attention_reference(w.q_rot, w.kv_cache, w.block_table, w.seq_lens,
+                                        w.centroids, num_kv_heads=8)
+    assert np.abs(out.cpu().numpy() - fo).max() <= 1e-4
+    assert np.abs(lse.cpu().numpy() - fl).max() <= 1e-4
+
+
 @pytest.mark.parametrize("layout", ["soa", "aos"])
 def test_backend_decode_entry(dev, layout):
     """``tq4_decode.{soa,aos}_decode.triton_turboquant_decode_attention`` with the backend's

@@ -569,18 +569,30 @@ __device__ __forceinline__ void load_q_rows(float4 (&qx)[8], const float *__rest
         qx[m] = *reinterpret_cast<const float4 *>(qr + d);
     }
 }
-__device__ __forceinline__ void q_operands(half8 (&bq)[8], const float4 (&qx)[8], int n, float scale) {
+// A q row whose largest |q * scale| reaches 2^15 is first scaled by the power of two 2^e
+// (e < 0) that puts it in [2^14, 2^15), inside the f16 range of the hi part; the returned
+// 2^-e (1 for every other row, so their scores are unchanged bit for bit) multiplies the
+// lane's dots.  The row's four lanes n, n + 16, n + 32, n + 48 share the maximum.
+__device__ __forceinline__ float q_operands(half8 (&bq)[8], const float4 (&qx)[8], int n, float scale) {
+    float amax = 0.f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+        amax = fmaxf(fmaxf(fmaxf(amax, fabsf(qx[m].x)), fmaxf(fabsf(qx[m].y), fabsf(qx[m].z))), fabsf(qx[m].w));
+    amax = rot_row_max(amax) * scale;
+    const int e = (amax >= 32768.f && amax < __builtin_inff()) ? 15 - __builtin_amdgcn_frexp_expf(amax) : 0;
+    const float rs = __builtin_ldexpf(scale, e);
     // the lane's part (hi for n < 8, lo for n >= 8) of two split values, packed
     const uint32_t sel = n >= 8 ? 0x07060302u : 0x05040100u;
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         const float4 x = qx[m];
-        const uint32_t s0 = split_f16(x.x * scale), s1 = split_f16(x.y * scale);
-        const uint32_t s2 = split_f16(x.z * scale), s3 = split_f16(x.w * scale);
+        const uint32_t s0 = split_f16(x.x * rs), s1 = split_f16(x.y * rs);
+        const uint32_t s2 = split_f16(x.z * rs), s3 = split_f16(x.w * rs);
         const uint32_t w0 = __builtin_amdgcn_perm(s1, s0, sel);
         const uint32_t w1 = __builtin_amdgcn_perm(s3, s2, sel);
         bq[m] = as_half8(w0, w0, w1, w1);
     }
+    return __builtin_ldexpf(1.f, -e);
 }
 
 // K-table entries of one tile's 16 code bytes (dims 32g + 2b, 32g + 2b + 1 for byte b),
@@ -1305,6 +1317,7 @@ void stage1_xdl_kernel(
     __shared__ __align__(16) float img[FUSED ? 4 : Cap::floats];  // FUSED writes no mid_o rows
     __shared__ __align__(16) float qbuf[ROT ? kRotGroupWaves * G * kQRowFloats : 4];
     half8 bq[8];
+    float q_unscale = 1.f;  // 2^-e of the lane's q row (q_operands)
 
     State st{__FLT_MAX__, 0.f, 0.f, 1.f};
     if (sinks && s_lo == 0) {
@@ -1399,10 +1412,11 @@ void stage1_xdl_kernel(
         for (int q = 0; q < TPL; ++q) {
             valid[q] = (uint32_t)(t0 + tok0 + q - cur_start) < (uint32_t)(cur_end - cur_start);
             if constexpr (LAYOUT == 0 || KF8) {
-                nf[q] = half_at(t.norm, q);
+                nf[q] = half_at(t.norm, q) * q_unscale;
             } else {
                 // ||c[idx]||^2 of token tok0 + q: totals sit in lanes n = token (any row)
-                nf[q] = half_at(t.norm, q) * __builtin_amdgcn_rsqf(__shfl(csq_tot, tok0 + q, kWave) + 1e-16f);
+                nf[q] = half_at(t.norm, q) * __builtin_amdgcn_rsqf(__shfl(csq_tot, tok0 + q, kWave) + 1e-16f) *
+                        q_unscale;
             }
         }
         if (k & 1)
@@ -1510,7 +1524,7 @@ void stage1_xdl_kernel(
         else if constexpr (!KF8)
             build_key_table<LAYOUT>(ktab, lut_rows, lane);
     }
-    q_operands(bq, q_rows, lc.n, score_scale_log2);
+    q_unscale = q_operands(bq, q_rows, lc.n, score_scale_log2);
     // one wave: its LDS writes complete before its later LDS reads; only the compiler must
     // keep the table lookups after the build
     asm volatile("" ::: "memory");

@@ -320,7 +320,10 @@ __global__ __launch_bounds__(kWave *W) __attribute__((amdgpu_waves_per_eu(W == k
     // then needs no fractional offset, and the 1.5 * 2^23 bias rounds it in the same fma
     const float kcell = floorf((mmin - 2.f * w) / w);
     const float y0 = kcell * w;
-    int cell_ok = fabsf(kcell) < 0x1p21f;
+    // the cell coordinate's rounding error grows like (|K| + 128) 2^-23 cells against the
+    // w / 64 widening of the windows: midpoints far from zero relative to their span (|K| >=
+    // 2^14; Lloyd-Max codebooks have |K| ~ 66) take the counting path
+    int cell_ok = fabsf(kcell) < 0x1p14f;
     if (threadIdx.x < kCells) {
         const int k = threadIdx.x;
         const float lo = y0 + ((float)k - 0.5f) * w - w * (1.f / 64), hi = y0 + ((float)k + 0.5f) * w + w * (1.f / 64);

@@ -585,6 +585,12 @@ class _CudaExtCompat:
     (``cuda/tq4_cuda_v7.cu:44-47``; it has no ``seq_lens`` argument), or only the non-empty
     splits when ``seq_lens`` is given; ``tq4_cuda_v7_full`` runs Stage1 and Stage2.  The
     object holds no state between calls.
+
+    Precondition of ``tq4_cuda_v7_stage2`` without ``seq_lens`` (the reference kernel's too):
+    Stage1 wrote every split row, i.e. every length gives S non-empty splits,
+    ``ceil(len / ceil(len / S)) == S`` (true when len is a multiple of S; 77 tokens over 32
+    splits of 3 leave 6 empty).  Rows of empty splits are never written (they keep whatever
+    the buffer held) and would enter the merge; otherwise pass ``seq_lens``.
     """
 
     def _stage1(self, q_rot, kv_cache, block_table, seq_lens, centroids, mid_o):
@@ -600,7 +606,8 @@ class _CudaExtCompat:
 
     def tq4_cuda_v7_stage2(self, mid_o, output, lse, seq_lens=None):
         if seq_lens is None:
-            # a length of S tokens over S splits makes every split non-empty
+            # every split merged (the caller's precondition: all of them were written); a
+            # length of S tokens over S splits makes every split non-empty
             seq_lens = torch.full((mid_o.size(0),), mid_o.size(2), dtype=torch.int32,
                                   device=mid_o.device)
         stage2(mid_o, seq_lens, output, lse)
