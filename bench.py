@@ -129,7 +129,8 @@ class HipEvents:
 
 def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4), slots_mode="random"):
     """Cache writer (SoA, bf16 K/V, norm correction) cold, kernel duration: one decode step
-    (64 tokens) and a prefill chunk (8192 tokens), 8 kv-heads.  ``bits``: key / value bits
+    (64 tokens), a prefill chunk (8192 tokens) and a long prefill (65536 tokens, 343 MB: the
+    writer's steady state), 8 kv-heads.  ``bits``: key / value bits
     (4/4: tq4_store; 3/4 and 3/3: tq4_store_preset).  Bytes per (token, kv-head): 2 x 256
     read + the slot written, plus 4 of slot mapping per token.  ``slots_mode``: "random"
     (the tokens scattered over the block pool: each block's metadata fields get their tokens
@@ -148,7 +149,7 @@ def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4), slots_mode="
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     rot, c, m = t(workloads.random_orthogonal(rng, 128)), t(cents), t(mids)
     out = {}
-    for name, n_tok in (("decode_b64", 64), ("prefill_n8192", 8192)):
+    for name, n_tok in (("decode_b64", 64), ("prefill_n8192", 8192), ("prefill_n65536", 65536)):
         if only is not None and name != only:
             continue
         key = torch.randn(n_tok, 8, 128, device=dev, dtype=torch.bfloat16)
@@ -509,7 +510,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--workload", default="stage1",
-                    choices=["stage1", "store_decode_b64", "store_prefill_n8192", "full_decode_b256",
+                    choices=["stage1", "store_decode_b64", "store_prefill_n8192", "store_prefill_n65536",
+                             "full_decode_b256",
                              "store_k3v4_prefill_n8192", "store_3bit_prefill_n8192", "stage1_ragged_b64",
                              "stage1_gqa8_b8_ctx32768", "stage2_b64_s32", "stage1_l2_resident",
                              *PRESET_WORKLOADS],
