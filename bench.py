@@ -214,6 +214,10 @@ def full_decode_time(dev, flush, timer, reps=30):
             "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes}
 
 
+# Stage1 side workloads of the 4-bit cache beside the headline
+GQA_WORKLOADS = ("stage1_ragged_b64", "stage1_gqa8_b8_ctx32768", "stage1_gqa6_b64_ctx4096",
+                 "stage1_gqa16_b64_ctx4096")
+
 # preset Stage1 workloads: name -> (preset, SoA record bytes, metadata fields)
 PRESET_WORKLOADS = {
     "stage1_fp8_b64_ctx4096": ("fp8", 192, 2),
@@ -273,9 +277,9 @@ def stage1_preset_time(dev, flush, timer, name, reps=30):
     return {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes}
 
 
-def stage1_workload_time(dev, flush, timer, w, reps=30):
-    """Stage1 (auto kernel, SoA) of another 4-bit workload, cold, kernel duration (median of
-    ``reps``); bytes as ``algorithmic_bytes``."""
+def stage1_workload_time(dev, flush, timer, w, reps=30, kernel="auto"):
+    """Stage1 (SoA; ``kernel``: auto, xdl or simple) of another 4-bit workload, cold, kernel
+    duration (median of ``reps``); bytes as ``algorithmic_bytes``."""
     import numpy as np
     import torch
 
@@ -289,7 +293,7 @@ def stage1_workload_time(dev, flush, timer, w, reps=30):
         flush.sum()
         a, b = timer.pair()
         timer.stamp_next_launch(a, b)
-        ops.stage1(q, c, bt, sl, lut, mid)
+        ops.stage1(q, c, bt, sl, lut, mid, kernel=kernel)
         torch.cuda.synchronize()
         if i >= 3:
             times.append(timer.elapsed_ms(a, b) * 1e3)
@@ -428,15 +432,20 @@ def side_workload(args, dev) -> int:
         metric = f"cache writer ({entry}, SoA, bf16 K/V, 8 kv-heads, {args.slots} slots) {size}: GB/s"
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = "bf16 in, f32 math"
-    elif args.workload in ("stage1_ragged_b64", "stage1_gqa8_b8_ctx32768"):
+    elif args.workload in GQA_WORKLOADS:
         from tq4_decode import workloads
 
-        w = workloads.ragged_b64() if args.workload == "stage1_ragged_b64" else workloads.gqa8_b8_ctx32768()
-        r = stage1_workload_time(dev, flush, timer, w, reps=args.steps)
+        make = {"stage1_ragged_b64": workloads.ragged_b64, "stage1_gqa8_b8_ctx32768": workloads.gqa8_b8_ctx32768,
+                "stage1_gqa6_b64_ctx4096": lambda: workloads.qwen3_4b_b64_ctx4096(num_q_heads=48),
+                "stage1_gqa16_b64_ctx4096": lambda: workloads.qwen3_4b_b64_ctx4096(num_q_heads=128)}
+        w = make[args.workload]()
+        r = stage1_workload_time(dev, flush, timer, w, reps=args.steps, kernel=args.kernel)
         us, gbs = r["us"], r["GBps"]
         metric = {"stage1_ragged_b64": "Stage1, B64 ragged (seq_lens 512..8192), 32/8 heads, 32 splits: GB/s",
-                  "stage1_gqa8_b8_ctx32768": "Stage1, B8 x ctx32768, 64/8 heads (GQA-8), 64 splits: GB/s"}[
-            args.workload]
+                  "stage1_gqa8_b8_ctx32768": "Stage1, B8 x ctx32768, 64/8 heads (GQA-8), 64 splits: GB/s",
+                  "stage1_gqa6_b64_ctx4096": "Stage1, B64 x ctx4096, 48/8 heads (GQA-6), 32 splits: GB/s",
+                  "stage1_gqa16_b64_ctx4096": "Stage1, B64 x ctx4096, 128/8 heads (GQA-16), 32 splits: GB/s"}[
+            args.workload] + ("" if args.kernel == "auto" else f" ({args.kernel} kernel)")
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = "4-bit K/V, f32 math"
     elif args.workload == "stage1_l2_resident":
@@ -513,7 +522,8 @@ def main() -> int:
                     choices=["stage1", "store_decode_b64", "store_prefill_n8192", "store_prefill_n65536",
                              "full_decode_b256",
                              "store_k3v4_prefill_n8192", "store_3bit_prefill_n8192", "stage1_ragged_b64",
-                             "stage1_gqa8_b8_ctx32768", "stage2_b64_s32", "stage1_l2_resident",
+                             "stage1_gqa8_b8_ctx32768", "stage1_gqa6_b64_ctx4096", "stage1_gqa16_b64_ctx4096",
+                             "stage2_b64_s32", "stage1_l2_resident",
                              *PRESET_WORKLOADS],
                     help="stage1: the headline (default); the others time only that workload "
                          "(--steps cold launches) and print its own JSON line, e.g. for a profile")

@@ -110,17 +110,19 @@ def random_orthogonal(rng, d):
     return (q * np.sign(np.diag(r))[None, :]).astype(np.float32)
 
 
-def qwen3_4b_b64_ctx4096(seed=20261201, batch=64, ctx=4096, num_splits=32):
+def qwen3_4b_b64_ctx4096(seed=20261201, batch=64, ctx=4096, num_splits=32, num_q_heads=32):
+    """The headline shape; ``num_q_heads`` other than 32 gives the same cache and block
+    table with GQA group num_q_heads / 8."""
     rng = np.random.default_rng(seed)
-    hk, hq, d, bs = 8, 32, 128, 16
+    hk, hq, d, bs = 8, num_q_heads, 128, 16
     blocks_per_seq = ctx // bs
     nblk = batch * blocks_per_seq
     q_rot = rng.standard_normal((batch, hq, d), dtype=np.float32)
     cache = synthetic_cache(rng, nblk, hk, d, bs)
     bt = rng.permutation(nblk).astype(np.int32).reshape(batch, blocks_per_seq)
     seq = np.full(batch, ctx, dtype=np.int32)
-    return Workload("qwen3_4b_b64_ctx4096", q_rot, cache, bt, seq, codebook.centroids(d, 4),
-                    num_splits, hk, bs)
+    name = "qwen3_4b_b64_ctx4096" if hq == 32 else f"gqa{hq // hk}_b64_ctx4096"
+    return Workload(name, q_rot, cache, bt, seq, codebook.centroids(d, 4), num_splits, hk, bs)
 
 
 def ragged_b64(seed=20261202, batch=64, lo=512, hi=8192, num_splits=32, max_blocks=512):
