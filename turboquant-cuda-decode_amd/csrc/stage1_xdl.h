@@ -184,6 +184,10 @@ struct LaneOffsets {
     uint32_t m;      // SoA: norm of the lane's first softmax token within its field array; AoS: its slot
     int tok_stride;  // bytes between consecutive tokens of one kv-head
     int mf;          // SoA: bytes between the three metadata arrays
+    // 3-bit presets, SoA (records staged through LDS): where the lane writes its 16 loaded
+    // bytes, reads its K bytes and its first V dword, and the byte shift that aligns a 3-bit
+    // V dword read from two LDS dwords
+    int kst, kld, vld, vsh;
 };
 
 // Bytes per (token, kv-head) record: SoA data record / AoS slot; KF8: the FP8-key preset
@@ -228,6 +232,20 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int h
     // V3: the 3 bytes of dims 8n .. 8n+7 (a dword read; its fourth byte lies inside the
     // record or, for n = 15, is the next record's / the metadata's first byte, masked off)
     o.v0 = 4 * g * pos + kvh * head + v_offset<LAYOUT, KF8, KB3>() + (V3 ? 3 : 4) * n;
+    if constexpr (KB3 && LAYOUT == 0) {
+        // Whole records instead: lane l < 8C loads bytes 16c .. 16c+15 (c = l % C, C = rec / 16
+        // lanes per record) of token l / C of the piece's first 8 tokens, and the same of token
+        // 8 + l / C in a second load; a spare lane l >= 8C loads and stores what lane l - 8C
+        // does (the same bytes to the same place).  In the LDS stage buffer record t sits at
+        // t * rec.
+        constexpr int R = record_bytes<LAYOUT, KF8, KB3, V3>(), C = R / 16;
+        const int lane = 16 * g + n, l = lane % (8 * C);
+        o.k = (l / C) * pos + kvh * head + 16 * (l % C);
+        o.kst = (l / C) * R + 16 * (l % C);
+        o.kld = n * R + 12 * g;
+        o.vld = 4 * g * R + kK3Bytes + (V3 ? (3 * n) & ~3 : 4 * n);
+        o.vsh = V3 ? (3 * n) & 3 : 0;
+    }
     if (LAYOUT == 0) {
         // metadata fields: K norm, V scale, V zero (KF8: V scale, V zero)
         o.m = (kvh * (KF8 ? 2 : 3) * block_size + st) * 2;  // plus the piece's metadata offset (soffset)
@@ -290,6 +308,44 @@ __device__ __forceinline__ RawK3 decode_k(const RawK3 &t, const LaneOffsets &o) 
     return r;
 }
 
+// 3-bit presets, SoA: the 112- or 96-byte records of a piece straddle 128-byte lines, which
+// a K load and separate V loads would each request (2.6 / 2.5 line requests per record,
+// against 1.75 / 1.5 when one load covers the whole record).  So the wave loads whole
+// records, 16 bytes per lane (tokens 0-7, then 8-15), and hands them over through LDS.
+struct RawRec {
+    uint4 a, b;
+};
+__device__ __forceinline__ void issue_k(RawRec &t, __amdgpu_buffer_rsrc_t rsrc, int doff, const LaneOffsets &o) {
+    t.a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
+    t.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff + 8 * o.tok_stride, 0));
+}
+// The records into the stage buffer, then the lane's K bytes (token n, bytes 12g ..) and its
+// V dwords (V dword n, or the 3-bit V bytes 3n .., of tokens 4g .. 4g+3) out of it.  One
+// wave's LDS accesses run in program order, so the reads see these writes and the next
+// piece's writes come after these reads.  The compiler barrier makes the compiler read
+// what the other lanes wrote (its per-lane view would forward a lane's own earlier values).
+template <int R, bool V3>
+__device__ __forceinline__ RawK3 stage_records(const RawRec &t, uint8_t *buf, const LaneOffsets &o,
+                                               uint32_t (&v)[4]) {
+    *reinterpret_cast<uint4 *>(buf + o.kst) = t.a;
+    *reinterpret_cast<uint4 *>(buf + o.kst + 8 * R) = t.b;
+    asm volatile("" ::: "memory");
+    const uint32_t *kp = reinterpret_cast<const uint32_t *>(buf + o.kld);
+    RawK3 k;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        k.w[i] = kp[i];
+    const uint32_t *vp = reinterpret_cast<const uint32_t *>(buf + o.vld);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (V3)
+            v[i] = __builtin_amdgcn_alignbyte(vp[i * R / 4 + 1], vp[i * R / 4], o.vsh);
+        else
+            v[i] = vp[i * R / 4];
+    }
+    return k;
+}
+
 template <int LAYOUT, int TPL, bool KF8 = false, bool KB3 = false, bool V3 = false>
 __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
                                         int moff, const LaneOffsets &o) {
@@ -315,9 +371,10 @@ __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rs
             }
         }
     } else if constexpr (LAYOUT == 0) {
+        if constexpr (!KB3)  // 3-bit presets: the V codes come with the whole records
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
+            for (int i = 0; i < 4; ++i)
+                t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
         if constexpr (TPL == 1) {
             t.norm = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff, 0);
             t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff + o.mf, 0);
@@ -708,20 +765,32 @@ __device__ __forceinline__ floatx4 pv_qk(floatx4 (&acc)[8], const uint32_t (&aw)
     const half8 a = as_half8(aw[0], aw[1], aw[2], aw[3]);
     floatx4 h = {0.f, 0.f, 0.f, 0.f}, l = {0.f, 0.f, 0.f, 0.f};
     if constexpr (V3) {
-        // codes of two tokens' dwords x, y at bit b -> (code_x << 7, code_y << 7) as u16 slots
-        auto pair = [](uint32_t x, uint32_t y, int b) {
-            const uint32_t cx = b >= 7 ? (x >> (b - 7)) : (x << (7 - b));
-            return (cx & 0x380u) | ((y << (23 - b)) & 0x03800000u);
+        // Two tokens' dwords x, y -> window w: (x bits 8w .. 8w+15) | (y bits 8w .. 8w+15) << 16,
+        // one v_perm; dims 0-4 of the lane lie in window 0, dims 5-7 in window 1.  A dim's code
+        // pair then sits at the same bit of both halves, and one shift and one mask move it to
+        // (code_x << 7, code_y << 7): a shift of d <= 7 bits carries the low half's upper bits
+        // only below bit 7 of the high half, a right shift of |d| <= 6 the high half's lower
+        // bits only above bit 9 of the low half, and the mask clears both.
+        uint32_t win[2][4];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t sel = w == 0 ? 0x05040100u : 0x06050201u;
+            win[w][0] = __builtin_amdgcn_perm(va[1], va[0], sel);
+            win[w][1] = __builtin_amdgcn_perm(va[3], va[2], sel);
+            win[w][2] = __builtin_amdgcn_perm(vb[1], vb[0], sel);
+            win[w][3] = __builtin_amdgcn_perm(vb[3], vb[2], sel);
+        }
+        auto codes = [&](int j, int i) {
+            const int w = j < 5 ? 0 : 1, d = 7 - (3 * j - 8 * w);
+            return (d >= 0 ? win[w][i] << d : win[w][i] >> -d) & 0x03800380u;
         };
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const int be = 6 * m, bo = 6 * m + 3;
+            const int je = 2 * m, jo = 2 * m + 1;
             h = mfma(k_operand(k, 2 * m), bq[2 * m], h);
-            acc[2 * m] = mfma(a, as_half8(pair(va[0], va[1], be), pair(va[2], va[3], be), pair(vb[0], vb[1], be),
-                                          pair(vb[2], vb[3], be)), acc[2 * m]);
+            acc[2 * m] = mfma(a, as_half8(codes(je, 0), codes(je, 1), codes(je, 2), codes(je, 3)), acc[2 * m]);
             l = mfma(k_operand(k, 2 * m + 1), bq[2 * m + 1], l);
-            acc[2 * m + 1] = mfma(a, as_half8(pair(va[0], va[1], bo), pair(va[2], va[3], bo), pair(vb[0], vb[1], bo),
-                                              pair(vb[2], vb[3], bo)), acc[2 * m + 1]);
+            acc[2 * m + 1] = mfma(a, as_half8(codes(jo, 0), codes(jo, 1), codes(jo, 2), codes(jo, 3)), acc[2 * m + 1]);
         }
         return h + l;
     }
@@ -1247,7 +1316,9 @@ void stage1_xdl_kernel(
     // q operands are built once the first tiles' loads are on their way.
     static_assert(!(KF8 && KB3), "one key format");
     static_assert(!V3 || (KB3 && !FUSED), "3-bit values come with 3-bit keys, not fused");
-    using RK = std::conditional_t<KF8, RawK8, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>;
+    // 3-bit presets, SoA: records staged through LDS (RawRec), see stage_records
+    constexpr bool STG = KB3 && LAYOUT == 0;
+    using RK = std::conditional_t<KF8, RawK8, std::conditional_t<STG, RawRec, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>>;
     LutRows lut_rows{};
     if constexpr (ROT) {
         // from the centroids themselves: entry e = (c[e & 15], c[e >> 4]), the pair-LUT row
@@ -1316,6 +1387,10 @@ void stage1_xdl_kernel(
     using Cap = SpanCap<LAYOUT, G, WPE>;
     __shared__ __align__(16) float img[FUSED ? 4 : Cap::floats];  // FUSED writes no mid_o rows
     __shared__ __align__(16) float qbuf[ROT ? kRotGroupWaves * G * kQRowFloats : 4];
+    // the stage buffer of the records (+ 16 bytes: a 3-bit V dword of token 15, n = 15, reads
+    // 4 bytes past them and masks them off)
+    constexpr int kRec = record_bytes<LAYOUT, KF8, KB3, V3>();
+    __shared__ __align__(16) uint8_t recbuf[STG ? 16 * kRec + 16 : 16];
     half8 bq[8];
     float q_unscale = 1.f;  // 2^-e of the lane's q row (q_operands)
 
@@ -1394,7 +1469,7 @@ void stage1_xdl_kernel(
     // Stage j: softmax of position j, then QK^T of position j + 1; odd stages also run
     // the PV of positions (j - 1, j).
     auto stage = [&](int k, const RawV<LAYOUT, TPL> &vprev, const RawV<LAYOUT, TPL> &vcur,
-                     const RK &kafter, int mask_lane, int j) {
+                     const RK &kafter, RawV<LAYOUT, TPL> &vafter, int mask_lane, int j) {
         // K-table lookups of the next tile first: their latency runs under the softmax
         KOps e;
         if constexpr (KF8)
@@ -1431,8 +1506,11 @@ void stage1_xdl_kernel(
         }
         if constexpr (LAYOUT == 1 && !KF8)
             csq_tot = sum_xor16(sum_xor32(e.csq));
-        // K bytes of position j + 2 into the MFMA layout (its load was issued 3 stages ago)
-        if constexpr (KF8 || KB3)
+        // K bytes of position j + 2 into the MFMA layout (its load was issued 3 stages ago);
+        // staged records also give its V codes
+        if constexpr (STG)
+            kn = stage_records<kRec, V3>(kafter, recbuf, off, vafter.v);
+        else if constexpr (KF8 || KB3)
             kn = decode_k(kafter, off);
         else
             kn = decode_k<LAYOUT>(kafter, off);
@@ -1538,6 +1616,9 @@ void stage1_xdl_kernel(
         if constexpr (KF8) {
             sc = qk_tile(lookup_tile(decode_k(kr[0], off), ktab), bq);
             kn = decode_k(kr[1], off);
+        } else if constexpr (STG) {
+            sc = qk_tile(lookup_tile<LAYOUT>(stage_records<kRec, V3>(kr[0], recbuf, off, vr[0].v), ktab), bq);
+            kn = stage_records<kRec, V3>(kr[1], recbuf, off, vr[1].v);
         } else if constexpr (KB3) {
             const KOps e = lookup_tile<LAYOUT>(decode_k(kr[0], off), ktab);
             sc = qk_tile(e, bq);
@@ -1557,7 +1638,7 @@ void stage1_xdl_kernel(
         do {
 #pragma unroll
             for (int k = 0; k < RING; ++k) {
-                stage(k, vr[(k + RING - 1) % RING], vr[k], kr[(k + 2) % RING], mask_lane, j + k);
+                stage(k, vr[(k + RING - 1) % RING], vr[k], kr[(k + 2) % RING], vr[(k + 2) % RING], mask_lane, j + k);
                 pos[(k + 1) % RING] = rsrc_at(base_lo, base_hi, min(j + k + 1 + RING, last));
                 issue_kpos(kr[(k + 1) % RING], pos[(k + 1) % RING]);
                 if (k & 1) {
