@@ -188,6 +188,7 @@ struct LaneOffsets {
     // bytes, reads its K bytes and its first V dword, and the byte shift that aligns a 3-bit
     // V dword read from two LDS dwords
     int kst, kld, vld, vsh;
+    uint32_t k1, k2;  // FP8 keys, SoA: the second and third 16-byte chunks the lane loads
 };
 
 // Bytes per (token, kv-head) record: SoA data record / AoS slot; KF8: the FP8-key preset
@@ -245,6 +246,20 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int n, int g, int kvh, int h
         o.kld = n * R + 12 * g;
         o.vld = 4 * g * R + kK3Bytes + (V3 ? (3 * n) & ~3 : 4 * n);
         o.vsh = V3 ? (3 * n) & 3 : 0;
+    }
+    if constexpr (KF8 && LAYOUT == 0) {
+        // FP8 keys, SoA: 192-byte records, 12 lanes each, 16 of them in three 16-byte-per-lane
+        // loads (chunk q = 64 i + lane of load i is bytes 16 (q % 12) .. of token q / 12);
+        // in the LDS stage buffer chunk q sits at 16 q
+        constexpr int R = record_bytes<LAYOUT, KF8, KB3, V3>(), C = R / 16;
+        const int lane = 16 * g + n;
+        auto chunk = [&](int q) { return (uint32_t)((q / C) * pos + kvh * head + 16 * (q % C)); };
+        o.k = chunk(lane);
+        o.k1 = chunk(64 + lane);
+        o.k2 = chunk(128 + lane);
+        o.kst = 16 * lane;
+        o.kld = n * R + 16 * g;
+        o.vld = 4 * g * R + kHeadDim + 4 * n;
     }
     if (LAYOUT == 0) {
         // metadata fields: K norm, V scale, V zero (KF8: V scale, V zero)
@@ -346,13 +361,26 @@ __device__ __forceinline__ RawK3 stage_records(const RawRec &t, uint8_t *buf, co
     return k;
 }
 
+// FP8 keys, SoA: the three loads of the staged records (see lane_offsets), then the lane's
+// 32 K bytes (token n, bytes 16g .. of each 64-byte half) and its V dwords out of LDS, as
+// stage_records does for the 3-bit presets.
+struct RawRec3 {
+    uint4 a, b, c;
+};
+__device__ __forceinline__ void issue_k(RawRec3 &t, __amdgpu_buffer_rsrc_t rsrc, int doff, const LaneOffsets &o) {
+    t.a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k, doff, 0));
+    t.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k1, doff, 0));
+    t.c = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, o.k2, doff, 0));
+}
+
 template <int LAYOUT, int TPL, bool KF8 = false, bool KB3 = false, bool V3 = false>
 __device__ __forceinline__ void issue_v(RawV<LAYOUT, TPL> &t, __amdgpu_buffer_rsrc_t rsrc, int doff,
                                         int moff, const LaneOffsets &o) {
     if constexpr (KF8) {  // no K norm: fields V scale, V zero (SoA); scale | zero after V (AoS)
+        if constexpr (LAYOUT == 1)  // SoA: the V codes come with the staged records
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
+            for (int i = 0; i < 4; ++i)
+                t.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, o.v0, doff + i * o.tok_stride, 0);
         if constexpr (LAYOUT == 0) {
             if constexpr (TPL == 1) {
                 t.scale = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o.m, moff, 0);
@@ -416,6 +444,18 @@ struct K8 {
 __device__ __forceinline__ K8 decode_k(const RawK8 &t, const LaneOffsets &o) {
     const RawK<0> h0{t.k}, h1{t.k2};
     return K8{decode_k<0>(h0, o), decode_k<0>(h1, o)};
+}
+__device__ __forceinline__ K8 stage_records(const RawRec3 &t, uint8_t *buf, const LaneOffsets &o, uint32_t (&v)[4]) {
+    *reinterpret_cast<uint4 *>(buf + o.kst) = t.a;
+    *reinterpret_cast<uint4 *>(buf + o.kst + 1024) = t.b;
+    *reinterpret_cast<uint4 *>(buf + o.kst + 2048) = t.c;
+    asm volatile("" ::: "memory");
+    const K8 k{*reinterpret_cast<const uint4 *>(buf + o.kld), *reinterpret_cast<const uint4 *>(buf + o.kld + 64)};
+    const uint32_t *vp = reinterpret_cast<const uint32_t *>(buf + o.vld);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        v[i] = vp[i * 48];  // token 4g + i: 192 bytes on
+    return k;
 }
 
 // V dwords and metadata of one tile; metadata as f16 pairs (token j in half j).
@@ -967,8 +1007,9 @@ __device__ __forceinline__ void softmax_tile(const float (&dot)[G / 4], const fl
 // HBM writes from breaking up the read stream.
 // The image takes what the K-code table leaves of a wave's share of the CU's 160 KB LDS
 // at WPE waves per SIMD.
-template <int LAYOUT, int G, int WPE> struct SpanCap {
-    static constexpr int bytes = 160 * 1024 / (4 * WPE) - KTable<LAYOUT>::words * 4;
+// RESERVED: the kernel's other LDS (K table, record stage buffer)
+template <int LAYOUT, int G, int WPE, int RESERVED> struct SpanCap {
+    static constexpr int bytes = 160 * 1024 / (4 * WPE) - RESERVED;
     static constexpr int row_floats = kHeadDim + 1;
     static constexpr int splits = (bytes / 4 / G) / row_floats;         // rows per head
     static constexpr int head_floats = (splits * row_floats + 3) & ~3;  // 16 B aligned
@@ -1318,7 +1359,9 @@ void stage1_xdl_kernel(
     static_assert(!V3 || (KB3 && !FUSED), "3-bit values come with 3-bit keys, not fused");
     // 3-bit presets, SoA: records staged through LDS (RawRec), see stage_records
     constexpr bool STG = KB3 && LAYOUT == 0;
-    using RK = std::conditional_t<KF8, RawK8, std::conditional_t<STG, RawRec, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>>;
+    // FP8 keys, SoA: records staged the same way (RawRec3)
+    constexpr bool STG8 = KF8 && LAYOUT == 0;
+    using RK = std::conditional_t<STG8, RawRec3, std::conditional_t<KF8, RawK8, std::conditional_t<STG, RawRec, std::conditional_t<KB3, RawK3, RawK<LAYOUT>>>>>;
     LutRows lut_rows{};
     if constexpr (ROT) {
         // from the centroids themselves: entry e = (c[e & 15], c[e >> 4]), the pair-LUT row
@@ -1384,13 +1427,15 @@ void stage1_xdl_kernel(
     lc.part_sel = lc.upper ? 0x07060302u : 0x05040100u;
 
     __shared__ uint32_t ktab[KTable<LAYOUT>::words];
-    using Cap = SpanCap<LAYOUT, G, WPE>;
+    // the stage buffer of the records (3-bit: + 16 bytes, a 3-bit V dword of token 15, n = 15,
+    // reads 4 bytes past them and masks them off); the image takes what the K table (none
+    // for FP8 keys) and the stage buffer leave
+    constexpr int kRec = record_bytes<LAYOUT, KF8, KB3, V3>();
+    constexpr int kStage = STG ? 16 * kRec + 16 : STG8 ? 16 * kRec : 0;
+    __shared__ __align__(16) uint8_t recbuf[kStage > 0 ? kStage : 16];
+    using Cap = SpanCap<LAYOUT, G, WPE, (KF8 ? 0 : KTable<LAYOUT>::words * 4) + kStage>;
     __shared__ __align__(16) float img[FUSED ? 4 : Cap::floats];  // FUSED writes no mid_o rows
     __shared__ __align__(16) float qbuf[ROT ? kRotGroupWaves * G * kQRowFloats : 4];
-    // the stage buffer of the records (+ 16 bytes: a 3-bit V dword of token 15, n = 15, reads
-    // 4 bytes past them and masks them off)
-    constexpr int kRec = record_bytes<LAYOUT, KF8, KB3, V3>();
-    __shared__ __align__(16) uint8_t recbuf[STG ? 16 * kRec + 16 : 16];
     half8 bq[8];
     float q_unscale = 1.f;  // 2^-e of the lane's q row (q_operands)
 
@@ -1510,6 +1555,8 @@ void stage1_xdl_kernel(
         // staged records also give its V codes
         if constexpr (STG)
             kn = stage_records<kRec, V3>(kafter, recbuf, off, vafter.v);
+        else if constexpr (STG8)
+            kn = stage_records(kafter, recbuf, off, vafter.v);
         else if constexpr (KF8 || KB3)
             kn = decode_k(kafter, off);
         else
@@ -1613,7 +1660,10 @@ void stage1_xdl_kernel(
         const int last = j0 + nchunk - 1;
         if (j0 > 0)
             open_chunk(j0, nchunk, last);
-        if constexpr (KF8) {
+        if constexpr (STG8) {
+            sc = qk_tile(lookup_tile(stage_records(kr[0], recbuf, off, vr[0].v), ktab), bq);
+            kn = stage_records(kr[1], recbuf, off, vr[1].v);
+        } else if constexpr (KF8) {
             sc = qk_tile(lookup_tile(decode_k(kr[0], off), ktab), bq);
             kn = decode_k(kr[1], off);
         } else if constexpr (STG) {
