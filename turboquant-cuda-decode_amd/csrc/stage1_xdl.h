@@ -1299,6 +1299,10 @@ void stage1_xdl_kernel(
     using QueryT = std::conditional_t<ROT == 1, __bf16, _Float16>;
     constexpr int TPL = G / 4;
     constexpr int RING = 4;
+    // ring slots of the first chunk issued before the K table and q operands are built (the
+    // rest after): with every wave of the launch asking at once, a wave's first tiles then
+    // queue behind fewer of the other waves' loads
+    constexpr int FIRST_SLOTS = 2;
     const int block_size = 1 << block_size_log2;
     int vh, wid, b;
     if constexpr (ROT) {
@@ -1575,7 +1579,18 @@ void stage1_xdl_kernel(
     RawV<LAYOUT, TPL> vr[RING];
     __amdgpu_buffer_rsrc_t pos[RING];
     // Lane tables of chunk [j0, j0 + 64) and the ring's first loads.
-    auto open_chunk = [&](int j0, int nchunk, int last) {
+    // ring slots k0 .. k1-1 of the chunk at j0: K and V loads of positions j0 + k
+    auto issue_slots = [&](int j0, int last, int k0, int k1) {
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+            if (k < k0 || k >= k1)
+                continue;
+            const auto rsrc = rsrc_at(base_lo, base_hi, min(j0 + k, last));
+            issue_kpos(kr[k], rsrc);
+            issue_vpos(vr[k], rsrc, moff_lane, min(j0 + k, last));
+        }
+    };
+    auto open_chunk = [&](int j0, int nchunk, int last, int nslots) {
         {
             const int p = j0 + min(lane, nchunk - 1);
             int base = 0;
@@ -1606,16 +1621,11 @@ void stage1_xdl_kernel(
             base_hi = (uint32_t)(a >> 32);
             moff_lane = (block_size - toff) * num_kv_heads * rec + toff * 2;
         }
-#pragma unroll
-        for (int k = 0; k < RING; ++k) {
-            const auto rsrc = rsrc_at(base_lo, base_hi, min(j0 + k, last));
-            issue_kpos(kr[k], rsrc);
-            issue_vpos(vr[k], rsrc, moff_lane, min(j0 + k, last));
-        }
+        issue_slots(j0, last, 0, nslots);
     };
 
-    // The first chunk's loads go out before the K table and the q operands are built.
-    open_chunk(0, min(64, total), min(64, total) - 1);
+    // The first chunk's first loads go out before the K table and the q operands are built.
+    open_chunk(0, min(64, total), min(64, total) - 1, FIRST_SLOTS);
     if constexpr (ROT) {
         // the sequence's rotated queries into qbuf (column tiles w, w + nvh, ... of this wave)
         half8 ah[G / 2][4];
@@ -1650,6 +1660,7 @@ void stage1_xdl_kernel(
             build_key_table<LAYOUT>(ktab, lut_rows, lane);
     }
     q_unscale = q_operands(bq, q_rows, lc.n, score_scale_log2);
+    issue_slots(0, min(64, total) - 1, FIRST_SLOTS, RING);
     // one wave: its LDS writes complete before its later LDS reads; only the compiler must
     // keep the table lookups after the build
     asm volatile("" ::: "memory");
@@ -1659,7 +1670,7 @@ void stage1_xdl_kernel(
         const int nchunk = min(64, total - j0);
         const int last = j0 + nchunk - 1;
         if (j0 > 0)
-            open_chunk(j0, nchunk, last);
+            open_chunk(j0, nchunk, last, RING);
         if constexpr (STG8) {
             sc = qk_tile(lookup_tile(stage_records(kr[0], recbuf, off, vr[0].v), ktab), bq);
             kn = stage_records(kr[1], recbuf, off, vr[1].v);
