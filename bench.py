@@ -226,12 +226,14 @@ PRESET_WORKLOADS = {
 }
 
 
-def stage1_preset_time(dev, flush, timer, name, reps=30):
+def stage1_preset_time(dev, flush, timer, name, reps=30, l2_resident=False):
     """Stage1 of a preset (FP8 keys: ``tq4_stage1_fp8``; 3-bit keys: ``tq4_stage1_preset``)
     at the B64 x ctx 4096 shape (32/8 heads, 32 splits), SoA, cold, kernel duration.
     Synthetic cache: random code bytes (E4M3 without NaN codes for FP8 keys), fp16 K norm /
     V scale / V zero in the ranges of the 4-bit workload.  Bytes: one slot per token and
-    kv-head + query + block table + mid_o rows."""
+    kv-head + query + block table + mid_o rows.  ``l2_resident``: every sequence's block
+    table points at the same 16 blocks, warmed into L2 by a launch before each timed one
+    (what the launch costs with HBM taken out; the bytes are the cold launch's)."""
     import numpy as np
     import torch
 
@@ -254,6 +256,8 @@ def stage1_preset_time(dev, flush, timer, name, reps=30):
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     q, c = t(w.q_rot), t(cache.reshape(nb, bs, hk, slot))
     bt, sl = t(w.block_table), t(w.seq_lens)
+    if l2_resident:
+        bt = (torch.arange(w.block_table.shape[1], dtype=torch.int32, device=dev) % 16).repeat(w.batch, 1)
     mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
     if preset == "fp8":
         run = lambda: ops.stage1_fp8(q, c, bt, sl, mid)  # noqa: E731
@@ -263,7 +267,10 @@ def stage1_preset_time(dev, flush, timer, name, reps=30):
                                         value_bits=preset[1])
     times = []
     for i in range(reps + 3):
-        flush.sum()
+        if l2_resident:
+            run()
+        else:
+            flush.sum()
         a, b = timer.pair()
         timer.stamp_next_launch(a, b)
         run()
@@ -412,12 +419,13 @@ def side_workload(args, dev) -> int:
     flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev).uniform_()
     timer = HipEvents(torch.cuda.current_stream(dev).cuda_stream)
     if args.workload in PRESET_WORKLOADS:
-        r = stage1_preset_time(dev, flush, timer, args.workload, reps=args.steps)
+        r = stage1_preset_time(dev, flush, timer, args.workload, reps=args.steps, l2_resident=args.l2_resident)
         us, gbs = r["us"], r["GBps"]
         preset = PRESET_WORKLOADS[args.workload][0]
         label = {"fp8": "FP8-key preset (turboquant_k8v4)", (3, 4): "3-bit-key preset (turboquant_k3v4_nc)",
                  (3, 3): "3-bit preset (turboquant_3bit_nc)"}[preset]
-        metric = f"Stage1, {label}, B64 x ctx4096 Qwen3-4B shape: GB/s"
+        metric = f"Stage1, {label}, B64 x ctx4096 Qwen3-4B shape: GB/s" + (
+            " (L2-resident: every block table on 16 blocks)" if args.l2_resident else "")
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = ("e4m3 K, 4-bit V" if preset == "fp8" else f"{preset[0]}-bit K, {preset[1]}-bit V") + ", f32 math"
     elif args.workload.startswith("store_"):
@@ -500,8 +508,10 @@ def side_workload(args, dev) -> int:
                       "steps": args.steps, "ms_per_step": round(us / 1e3, 5),
                       "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                       "dtype": dtype, "data": "synthetic",
-                      "config": {"workload": args.workload}, "timing": timing,
-                      "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}))
+                      "config": {"workload": args.workload, **({"l2_resident": True} if args.l2_resident else {})},
+                      "timing": timing,
+                      # an L2-resident run reads no HBM: its GB/s are the cold launch's bytes over its time
+                      "pct_of_hbm_peak": None if args.l2_resident else round(100 * gbs / HBM_PEAK_GBS, 2)}))
     return 0
 
 
@@ -515,6 +525,8 @@ def main() -> int:
                     help="writer workloads: token slots scattered over the pool, or in order")
     ap.add_argument("--kernel", default="auto", choices=["auto", "simple", "xdl"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--l2-resident", action="store_true",
+                    help="preset workloads: every block table on 16 blocks kept in L2 (HBM taken out)")
     ap.add_argument("--no-variants", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (PMC byte-counter calibration)")
