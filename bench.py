@@ -466,22 +466,24 @@ def side_workload(args, dev) -> int:
         # when HBM is taken out of the picture
         w = workloads.qwen3_4b_b64_ctx4096()
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-        q, c, sl, lut = t(w.q_rot), t(w.kv_cache), t(w.seq_lens), t(w.pair_lut)
+        q, sl, lut = t(w.q_rot), t(w.seq_lens), t(w.pair_lut)
+        c = t(w.kv_cache if args.layout == "soa" else workloads.soa_to_aos(w.kv_cache, w.centroids, w.num_kv_heads))
         bt16 = (torch.arange(w.block_table.shape[1], dtype=torch.int32, device=dev) % 16).repeat(w.batch, 1)
         mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
         times = []
         for i in range(args.steps + 3):
-            ops.stage1(q, c, bt16, sl, lut, mid)  # warms L2 with the 16 blocks
+            ops.stage1(q, c, bt16, sl, lut, mid, layout=args.layout)  # warms L2 with the 16 blocks
             a, b = timer.pair()
             timer.stamp_next_launch(a, b)
-            ops.stage1(q, c, bt16, sl, lut, mid)
+            ops.stage1(q, c, bt16, sl, lut, mid, layout=args.layout)
             torch.cuda.synchronize()
             if i >= 3:
                 times.append(timer.elapsed_ms(a, b) * 1e3)
             timer.destroy(a, b)
         us = round(statistics.median(times), 2)
         gbs = round(algorithmic_bytes(w) / us / 1e3, 1)
-        metric = "Stage1, headline shape, every KV read an L2 hit (16 shared blocks): headline bytes / time, GB/s"
+        metric = (f"Stage1, headline shape ({args.layout.upper()}), every KV read an L2 hit (16 shared blocks): "
+                  "headline bytes / time, GB/s")
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = "4-bit K/V, f32 math"
     elif args.workload == "stage2_b64_s32":
