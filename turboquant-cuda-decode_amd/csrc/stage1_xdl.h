@@ -184,11 +184,11 @@ struct LaneOffsets {
     uint32_t m;      // SoA: norm of the lane's first softmax token within its field array; AoS: its slot
     int tok_stride;  // bytes between consecutive tokens of one kv-head
     int mf;          // SoA: bytes between the three metadata arrays
-    // 3-bit presets, SoA (records staged through LDS): where the lane writes its 16 loaded
-    // bytes, reads its K bytes and its first V dword, and the byte shift that aligns a 3-bit
-    // V dword read from two LDS dwords
+    // SoA records of the presets, staged through LDS: where the lane writes its first 16
+    // loaded bytes, reads its K bytes and its first V dword, and the byte shift that aligns a
+    // 3-bit V dword read from two LDS dwords
     int kst, kld, vld, vsh;
-    uint32_t k1, k2;  // FP8 keys, SoA: the second and third 16-byte chunks the lane loads
+    uint32_t k1, k2;  // FP8 keys: the second and third 16-byte chunks the lane loads
 };
 
 // Bytes per (token, kv-head) record: SoA data record / AoS slot; KF8: the FP8-key preset
