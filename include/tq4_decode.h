@@ -73,9 +73,9 @@ int tq4_stage1(const float *q_rot, const uint8_t *kv_cache, const int32_t *block
 
 /* Same as tq4_stage1 with an explicit kernel choice (TQ4_KERNEL_*): SIMPLE is the
  * plain-VALU kernel (GQA group 1, 2, 4, 6, 8 or 16); XDL (v_mfma_f32_16x16x32_f16) is the
- * matrix-core kernel (GQA group 3 or more: waves of 4 q-heads for groups up to 4, else
- * parts of 8 q-heads; block_size a power of two >= 16, cache_block_stride a multiple of
- * 16).  AUTO picks XDL when it applies, SIMPLE
+ * matrix-core kernel (any GQA group: waves of 4 q-heads for groups up to 4, else parts of
+ * 8 q-heads, padding heads where the group does not fill them; block_size a power of two
+ * >= 16, cache_block_stride a multiple of 16).  AUTO picks XDL when it applies, SIMPLE
  * otherwise.  sinks (fp32 [Hq], may be NULL): per-head sink logits in the score domain
  * (q.k * attn_scale); split 0 starts its softmax with max = sink, sum = 1.
  * Replaces: the per-version entry points tq4_cuda_v1 .. tq4_cuda_v9 (cuda/tq4_cuda_vN_bind.cpp);
@@ -166,8 +166,8 @@ int tq4_store(const void *key, const void *value, int dtype, const int32_t *slot
  * dim (record 128 K bytes | 64 V bytes, SoA metadata fields V scale and V zero; AoS slot
  * 196 bytes = K | V | scale | zero).  query is the unrotated query (fp32 [B, Hq, D]);
  * score = q.k * attn_scale.  Same mid_o contract, grid rule and sinks as tq4_stage1_ex;
- * runs on the 16x16x32 MFMA kernel where it applies (GQA group 3 or more, power-of-two
- * block_size >= 16, 16-byte block stride), else on the VALU kernel.
+ * runs on the 16x16x32 MFMA kernel where it applies (power-of-two block_size >= 16,
+ * 16-byte block stride), else on the VALU kernel.
  * Replaces: _tq_decode_stage1 with KEY_FP8=1, reference/soa_decode_v1.py:213-230 (launch
  *           :519-606); the AoS kernel reference/aos_decode.py.
  */
@@ -200,9 +200,8 @@ int tq4_store_fp8(const void *key, const void *value, int dtype, const int32_t *
  * fp16 metadata fields K norm (folded norm correction), V scale, V zero; AoS slot
  * K | fp16 norm | V | fp16 scale | fp16 zero padded to even (118 bytes for 3/4, 102 for 3/3).
  * centroids: the 2^key_bits Lloyd-Max centroids.  Same mid_o contract, grid rule and sinks
- * as tq4_stage1_ex; 3/4 and 3/3 run on the 16x16x32 MFMA kernel where it applies (GQA group
- * 3 or more, power-of-two block_size >= 16, 16-byte block stride), everything else on the
- * VALU kernel.
+ * as tq4_stage1_ex; 3/4 and 3/3 run on the 16x16x32 MFMA kernel where it applies
+ * (power-of-two block_size >= 16, 16-byte block stride), everything else on the VALU kernel.
  * Replaces: _tq_decode_stage1 with MSE_BITS = 3 / VQB = 3, reference/soa_decode_v1.py:122-132
  *           (3-bit K unpack) and :271-284 (3-bit V unpack); the AoS kernel
  *           reference/aos_decode.py:121-285.

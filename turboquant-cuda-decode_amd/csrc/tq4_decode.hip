@@ -282,19 +282,19 @@ template <int LAYOUT> int dispatch_simple(const Stage1Args &a, hipStream_t st) {
     return launch_status("stage1_simple");
 }
 
-// GQA groups of 3 and more: groups up to 4 on 4-head waves, larger ones in parts of 8 heads
-// (6: one part with two padding heads; 16: two parts).  Groups of 1 and 2 would leave most of
-// the matrix-core columns idle and run on the VALU kernel.
+// Every GQA group: groups up to 4 on 4-head waves (1, 2 and 3 with padding heads: each KV
+// tile is still read and looked up once per wave, so MHA and GQA-2 take about the headline's
+// time, 1.4-1.5x faster than the VALU kernel), larger ones in parts of 8 heads (6: one part
+// with two padding heads; 16: two parts).
 bool mfma_applies(const Stage1Args &a) {
-    const int g = a.Hq / a.Hk;
     const bool pow2 = a.bs >= 16 && (a.bs & (a.bs - 1)) == 0;
-    return g >= 3 && pow2 && a.stride % 16 == 0;
+    return pow2 && a.stride % 16 == 0;
 }
 
 template <int LAYOUT> int dispatch_xdl(const Stage1Args &a, hipStream_t st) {
     if (!mfma_applies(a))
-        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: XDL kernel needs a GQA group of 3 or more, a "
-                                       "power-of-two block_size >= 16 and a 16-byte block stride");
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: XDL kernel needs a power-of-two block_size >= 16 "
+                                       "and a 16-byte block stride");
     if (xdl_heads(a) == 4)
         launch_xdl<LAYOUT, 4>(a, st);
     else

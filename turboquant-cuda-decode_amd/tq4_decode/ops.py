@@ -468,8 +468,8 @@ def turboquant_decode_attention(query, kv_cache, block_table, seq_lens, Pi, cent
     (``reference/turboquant_attn.py:368-373``).  ``sinks`` (fp32 ``[Hq]``) enter split 0.
     Built for the 4-bit ``turboquant_4bit_nc`` cache, with ``key_fp8`` the ``turboquant_k8v4``
     cache (unrotated query), and the 3-bit presets ``turboquant_k3v4_nc`` /
-    ``turboquant_3bit_nc``, all on the 16x16x32 MFMA Stage1 where it applies (GQA group >= 3),
-    else the VALU kernel; 4-bit AoS without norm correction raises ``NotImplementedError``.
+    ``turboquant_3bit_nc``, all on the 16x16x32 MFMA Stage1 where it applies (power-of-two
+    blocks of 16 tokens or more), else the VALU kernel; 4-bit AoS without norm correction raises ``NotImplementedError``.
     """
     _require(query.dim() == 3 and query.size(2) == HEAD_DIM, f"query must be [B, Hq, {HEAD_DIM}]")
     S = int(max_num_kv_splits)
