@@ -216,7 +216,7 @@ def full_decode_time(dev, flush, timer, reps=30):
 
 # Stage1 side workloads of the 4-bit cache beside the headline
 GQA_WORKLOADS = ("stage1_ragged_b64", "stage1_gqa8_b8_ctx32768", "stage1_gqa6_b64_ctx4096",
-                 "stage1_gqa16_b64_ctx4096")
+                 "stage1_gqa16_b64_ctx4096", "stage1_mha_b64_ctx4096", "stage1_gqa2_b64_ctx4096")
 
 # preset Stage1 workloads: name -> (preset, SoA record bytes, metadata fields)
 PRESET_WORKLOADS = {
@@ -445,14 +445,18 @@ def side_workload(args, dev) -> int:
 
         make = {"stage1_ragged_b64": workloads.ragged_b64, "stage1_gqa8_b8_ctx32768": workloads.gqa8_b8_ctx32768,
                 "stage1_gqa6_b64_ctx4096": lambda: workloads.qwen3_4b_b64_ctx4096(num_q_heads=48),
-                "stage1_gqa16_b64_ctx4096": lambda: workloads.qwen3_4b_b64_ctx4096(num_q_heads=128)}
+                "stage1_gqa16_b64_ctx4096": lambda: workloads.qwen3_4b_b64_ctx4096(num_q_heads=128),
+                "stage1_mha_b64_ctx4096": lambda: workloads.qwen3_4b_b64_ctx4096(num_q_heads=8),
+                "stage1_gqa2_b64_ctx4096": lambda: workloads.qwen3_4b_b64_ctx4096(num_q_heads=16)}
         w = make[args.workload]()
         r = stage1_workload_time(dev, flush, timer, w, reps=args.steps, kernel=args.kernel)
         us, gbs = r["us"], r["GBps"]
         metric = {"stage1_ragged_b64": "Stage1, B64 ragged (seq_lens 512..8192), 32/8 heads, 32 splits: GB/s",
                   "stage1_gqa8_b8_ctx32768": "Stage1, B8 x ctx32768, 64/8 heads (GQA-8), 64 splits: GB/s",
                   "stage1_gqa6_b64_ctx4096": "Stage1, B64 x ctx4096, 48/8 heads (GQA-6), 32 splits: GB/s",
-                  "stage1_gqa16_b64_ctx4096": "Stage1, B64 x ctx4096, 128/8 heads (GQA-16), 32 splits: GB/s"}[
+                  "stage1_gqa16_b64_ctx4096": "Stage1, B64 x ctx4096, 128/8 heads (GQA-16), 32 splits: GB/s",
+                  "stage1_mha_b64_ctx4096": "Stage1, B64 x ctx4096, 8/8 heads (MHA), 32 splits: GB/s",
+                  "stage1_gqa2_b64_ctx4096": "Stage1, B64 x ctx4096, 16/8 heads (GQA-2), 32 splits: GB/s"}[
             args.workload] + ("" if args.kernel == "auto" else f" ({args.kernel} kernel)")
         timing = "kernel start/end stamped by hipExtLaunchKernel events, median"
         dtype = "4-bit K/V, f32 math"
@@ -537,6 +541,7 @@ def main() -> int:
                              "full_decode_b256",
                              "store_k3v4_prefill_n8192", "store_3bit_prefill_n8192", "stage1_ragged_b64",
                              "stage1_gqa8_b8_ctx32768", "stage1_gqa6_b64_ctx4096", "stage1_gqa16_b64_ctx4096",
+                             "stage1_mha_b64_ctx4096", "stage1_gqa2_b64_ctx4096",
                              "stage2_b64_s32", "stage1_l2_resident",
                              *PRESET_WORKLOADS],
                     help="stage1: the headline (default); the others time only that workload "
