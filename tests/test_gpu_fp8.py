@@ -74,10 +74,11 @@ def _assert_parity(got, ref, tol=1e-4):
 
 
 @pytest.mark.parametrize("layout", ["soa", "aos"])
-@pytest.mark.parametrize("group,kernel", [(1, "auto"), (4, "simple"), (4, "xdl"), (6, "xdl"), (8, "simple"),
-                                          (8, "xdl"), (16, "auto"), (16, "simple")])
+@pytest.mark.parametrize("group,kernel", [(1, "auto"), (1, "simple"), (2, "xdl"), (4, "simple"), (4, "xdl"),
+                                          (6, "xdl"), (8, "simple"), (8, "xdl"), (16, "auto"), (16, "simple")])
 def test_stage1_fp8_matches_oracle(dev, layout, group, kernel):
-    """GQA 3 and more run on the 16x16x32 MFMA kernel under auto; both kernels are checked."""
+    """Every group runs on the 16x16x32 MFMA kernel under auto (1 and 2 in 4-head waves with
+    padding heads); both kernels are checked."""
     hk = 4
     w, cache, query = _fp8_workload(302, [1, 37, 600, 1025], 8, hq=hk * group, hk=hk, layout=layout)
     got = _stage1(dev, w, cache, query, 8, layout, kernel=kernel)
