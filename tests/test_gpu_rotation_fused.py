@@ -11,7 +11,7 @@ The fused path leaves the q_rot workspace unwritten (NaN-prefilled here), which 
 that it ran; fp32 queries keep the rotation launch (the workspace is written).
 
 Shapes: (kv-heads, GQA group) with one, two, four and eight waves per sequence, groups with
-padding heads (3, 6) and two parts per kv-head (16); rows of very large and very small
+padding heads (3, 6), two parts per kv-head (16) and four (MQA: one kv-head, 32 q-heads); rows of very large and very small
 magnitude; empty and one-token sequences; sinks.
 """
 import numpy as np
@@ -50,7 +50,7 @@ def _separate(dev, q, r, cache, bt, sl, cents, out_dtype, sinks):
 # (kv-heads, group, batch): batch * kv-heads * parts fills the device (2048 waves), so the
 # step takes the one-split path
 SHAPES = [(8, 4, 256), (8, 8, 256), (8, 3, 256), (8, 6, 256), (4, 16, 256), (4, 4, 512), (2, 8, 1024),
-          (1, 8, 2048)]
+          (1, 8, 2048), (1, 32, 512)]
 
 
 @pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16])

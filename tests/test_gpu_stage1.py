@@ -61,11 +61,12 @@ def test_ragged_with_empty_and_partial_splits(dev, kernel, layout):
 
 @pytest.mark.parametrize("kernel,group", [("simple", 1), ("simple", 2), ("simple", 4), ("simple", 6),
                                           ("simple", 8), ("simple", 16), ("xdl", 1), ("xdl", 2),
-                                          ("xdl", 3), ("xdl", 4), ("xdl", 6), ("xdl", 8), ("xdl", 12),
-                                          ("xdl", 16)])
+                                          ("xdl", 3), ("xdl", 4), ("xdl", 5), ("xdl", 6), ("xdl", 8),
+                                          ("xdl", 12), ("xdl", 16), ("xdl", 32)])
 def test_gqa_groups(dev, kernel, group):
     """The matrix-core kernel serves a group in waves of 4 (groups up to 4) or 8 q-heads:
-    1, 2, 3 and 6 leave padding heads in their wave, 12 and 16 take two waves per kv-head."""
+    1, 2, 3, 5 and 6 leave padding heads in their wave, 12 and 16 take two waves per
+    kv-head, 32 four."""
     hk = 4
     w = workloads.small(102, 3, [77, 300, 1024], 7, num_q_heads=hk * group, num_kv_heads=hk)
     assert_parity(run(w, dev, kernel), oracle(w))
