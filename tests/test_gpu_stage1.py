@@ -230,6 +230,17 @@ def test_wave_deal_over_several_lane_chunks(dev, layout, group):
     assert_parity(run(w, dev, "xdl", layout, cache), oracle(w, layout, cache))
 
 
+def test_runs_of_more_than_64_splits(dev):
+    # 72 sequences x 8 kv-heads x 2 parts (GQA-16) = 1152 (sequence, part) pairs: one wave
+    # each, so a sequence's wave runs all its live splits -- up to 80 here, past the 64 a
+    # wave keeps in its lanes -- next to sequences of fewer splits and an empty one
+    rng = np.random.default_rng(111)
+    lens = np.concatenate([rng.integers(65, 81, size=24), rng.integers(200, 241, size=24),
+                           rng.integers(1, 60, size=23), [0]])
+    w = workloads.small(111, 72, lens, 80, num_q_heads=8 * 16, num_kv_heads=8)
+    assert_parity(run(w, dev, "xdl"), oracle(w))
+
+
 def test_wave_deal_gives_a_lone_long_sequence_many_waves(dev):
     # two live sequences out of 64: the deal hands the long one up to one wave per split
     lens = [0] * 64

@@ -503,6 +503,7 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
 // (deal_ranked).
 struct Deal {
     int b, wid, nw;  // b < 0: the deal leaves this wave without work
+    int len;         // seq_lens[b], as the deal read it
 };
 
 // Live splits and estimated stream positions of sequence bb (0 past the batch): each
@@ -510,12 +511,13 @@ struct Deal {
 struct SeqLoad {
     int live;
     uint32_t est;
+    int len;
 };
 __device__ __forceinline__ SeqLoad sequence_load(const int32_t *__restrict__ seq_lens, int B, int S, int bb) {
     const int len = bb < B ? max(seq_lens[bb], 0) : 0;
     const int split_len = (len + S - 1) / S;
     const int live = split_len > 0 ? (len + split_len - 1) / split_len : 0;
-    return SeqLoad{live, (uint32_t)live * (uint32_t)(((split_len + 15) >> 4) + 1)};
+    return SeqLoad{live, (uint32_t)live * (uint32_t)(((split_len + 15) >> 4) + 1), len};
 }
 
 // Inclusive prefix sum over the wave's 64 lanes: shifts within each 16-lane row, then the
@@ -570,7 +572,7 @@ __device__ Deal deal_ranked(const int32_t *__restrict__ seq_lens, int B, int S, 
     const int T = nw * B;
     const int p = (T % 2 == 0 && x >= T / 2) ? 3 * T / 2 - 1 - x : x;
     if ((uint32_t)p >= wave_sum((uint32_t)k))
-        return Deal{-1, 0, 0};
+        return Deal{-1, 0, 0, -1};
     auto count_ge = [&](uint32_t t) {
         return wave_sum((uint32_t)((n_hi > 0 && l_hi >= t ? n_hi : 0) + (n_lo > 0 && l_lo >= t ? n_lo : 0)));
     };
@@ -591,7 +593,7 @@ __device__ Deal deal_ranked(const int32_t *__restrict__ seq_lens, int B, int S, 
     const int sq = __builtin_ctzll(hit);
     const int j0 = idx - __builtin_amdgcn_readlane(excl, sq);
     const int j = __builtin_amdgcn_readlane(hi_in ? 1 : 0, sq) ? j0 : __builtin_amdgcn_readlane(r, sq) + j0;
-    return Deal{sq, j, __builtin_amdgcn_readlane(k, sq)};
+    return Deal{sq, j, __builtin_amdgcn_readlane(k, sq), __builtin_amdgcn_readlane(q.len, sq)};
 }
 
 __device__ Deal deal_waves(const int32_t *__restrict__ seq_lens, int B, int S, int nw, int x, int lane) {
@@ -603,7 +605,7 @@ __device__ Deal deal_waves(const int32_t *__restrict__ seq_lens, int B, int S, i
         equal = equal && __ballot(bb < B && seq_lens[bb] != len0) == 0;
     }
     if (equal)
-        return Deal{x / nw, x % nw, nw};
+        return Deal{x / nw, x % nw, nw, len0};
     if (B <= kWave)
         return deal_ranked(seq_lens, B, S, nw, x, lane);
     const SeqLoad first = sequence_load(seq_lens, B, S, lane);
@@ -629,12 +631,13 @@ __device__ Deal deal_waves(const int32_t *__restrict__ seq_lens, int B, int S, i
         const uint64_t hit = __ballot(x >= w_in && x < w_out);
         if (hit) {
             const int l = __builtin_ctzll(hit);
-            return Deal{c0 + l, x - __builtin_amdgcn_readlane(w_in, l), __builtin_amdgcn_readlane(mine, l)};
+            return Deal{c0 + l, x - __builtin_amdgcn_readlane(w_in, l), __builtin_amdgcn_readlane(mine, l),
+                        __builtin_amdgcn_readlane(q.len, l)};
         }
         est_carry = (uint32_t)__builtin_amdgcn_readlane((int)est_out, kWave - 1);
         wave_carry = __builtin_amdgcn_readlane(w_out, kWave - 1);
     }
-    return Deal{-1, 0, 0};
+    return Deal{-1, 0, 0, -1};
 }
 
 // Running softmax state of a lane: the shared max of its head (as -m, exp2 domain;
@@ -1377,7 +1380,11 @@ void stage1_xdl_kernel(
     } else if constexpr (!KF8 && !KB3) {
         lut_rows = load_lut_rows(pair_lut, lane);
     }
+    // the head's sink logit (a dummy read when there are none: one unconditional load here
+    // keeps the waits before the first KV loads from covering it)
+    const float sink = *(sinks ? sinks + hb + hl : q_rot);
     int run_waves = nw;  // waves sharing this wave's sequence and kv-head
+    int dealt_len = 0;
     if constexpr (!FUSED) {
         const Deal d = deal_waves(seq_lens, gridDim.z, num_splits, nw, wid + nw * b, lane);
         if (d.b < 0)
@@ -1385,20 +1392,9 @@ void stage1_xdl_kernel(
         b = d.b;
         wid = d.wid;
         run_waves = d.nw;
+        dealt_len = d.len;
     }
-    float4 q_rows[8];
-    RotRows<G> rot_rows;
-    RotCols rot_cols;
-    const int nvh = ROT ? (int)(blockDim.x / kWave) : 1;
-    if constexpr (ROT) {
-        // the rotation's loads go out before the first KV loads (their wait then skips those)
-        rot_load_rows<QueryT, G>(rot_rows, static_cast<const QueryT *>(query), (int64_t)b * num_q_heads,
-                                 num_q_heads, lane & 15, lane >> 4);
-        rot_load_cols(rot_cols, rot_t, threadIdx.x / kWave, lane & 15, lane >> 4);
-    } else {
-        load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + hb + hl, lane >> 4, KF8);
-    }
-    const int seq_len = seq_lens[b];
+    const int seq_len = FUSED ? seq_lens[b] : dealt_len;
     // split partition: L = ceil(len / S); live splits are those with s * L < len
     const int split_len = (seq_len + num_splits - 1) / num_splits;
     const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
@@ -1437,7 +1433,10 @@ void stage1_xdl_kernel(
     constexpr int kRec = record_bytes<LAYOUT, KF8, KB3, V3>();
     constexpr int kStage = STG ? 16 * kRec + 16 : STG8 ? 16 * kRec : 0;
     __shared__ __align__(16) uint8_t recbuf[kStage > 0 ? kStage : 16];
-    using Cap = SpanCap<LAYOUT, G, WPE, (KF8 ? 0 : KTable<LAYOUT>::words * 4) + kStage>;
+    // split starts of a chunk, one byte per stream position (chunk_tiles; one split per wave
+    // when FUSED)
+    __shared__ uint8_t marks[FUSED ? 1 : kWave];
+    using Cap = SpanCap<LAYOUT, G, WPE, (KF8 ? 0 : KTable<LAYOUT>::words * 4) + kStage + (FUSED ? 0 : kWave)>;
     __shared__ __align__(16) float img[FUSED ? 4 : Cap::floats];  // FUSED writes no mid_o rows
     __shared__ __align__(16) float qbuf[ROT ? kRotGroupWaves * G * kQRowFloats : 4];
     half8 bq[8];
@@ -1447,7 +1446,7 @@ void stage1_xdl_kernel(
     if (sinks && s_lo == 0) {
         // split 0 starts from the head's sink logit: max = sink, sum = 1 (one lane per head,
         // lane h, holds it; the sums are totalled over the lanes n = h (mod G))
-        st.negm = -sinks[(int64_t)hb + hl] * kLog2e;
+        st.negm = -sink * kLog2e;
         st.l = lane < G ? 1.f : 0.f;
     }
     floatx4 acc[8];
@@ -1462,9 +1461,26 @@ void stage1_xdl_kernel(
         const int st0 = s * split_len, en = min(st0 + split_len, seq_len);
         return ((en - 1) >> 4) - (st0 >> 4) + 1;
     };
+    // A run of at most 64 splits keeps them in lanes (lane i: split s_lo + i): first tile,
+    // tile count and the stream position where the split starts.  Lane-parallel, this takes a
+    // few instructions where loops over the splits took hundreds (all of a CU's waves run
+    // their prologue at once).
+    const int n_run = s_hi - s_lo;
+    const bool run_in_lanes = n_run <= kWave;
+    int sp_tf = 0, sp_nt = 0, sp_base = 0;
     int total = 0;
-    for (int s = s_lo; s < s_hi; ++s)
-        total += (split_tiles(s) + 1) & ~1;
+    if (run_in_lanes) {
+        const int st0 = (s_lo + min(lane, n_run - 1)) * split_len, en = min(st0 + split_len, seq_len);
+        sp_tf = st0 >> 4;
+        sp_nt = ((en - 1) >> 4) - sp_tf + 1;
+        const int e = lane < n_run ? (sp_nt + 1) & ~1 : 0;
+        const int incl = (int)wave_scan((uint32_t)e);
+        sp_base = incl - e;
+        total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    } else {
+        for (int s = s_lo; s < s_hi; ++s)
+            total += (split_tiles(s) + 1) & ~1;
+    }
     const int tail = ((total + RING - 1) & ~(RING - 1)) - total;
     total += tail;
     auto split_stop = [&](int s) { return ((split_tiles(s) + 1) & ~1) + (s == s_hi - 1 ? tail : 0); };
@@ -1590,8 +1606,32 @@ void stage1_xdl_kernel(
             issue_vpos(vr[k], rsrc, moff_lane, min(j0 + k, last));
         }
     };
-    auto open_chunk = [&](int j0, int nchunk, int last, int nslots) {
-        {
+    // Lane i: the tile and mask of stream position j0 + i and the block-table entry of that
+    // tile (read here; the addresses come from chunk_addresses).
+    auto chunk_tiles = [&](int j0, int nchunk) {
+        if (run_in_lanes) {
+            int i = 0;  // the lane's split, as an index into the run
+            if constexpr (!FUSED) {
+                if (n_run > 1) {
+                    // the splits that start inside (j0, j0 + 64) mark their offset; position
+                    // j0 + q lies in the split that holds j0, moved on by the marks up to q
+                    marks[lane] = 0;
+                    const int q = sp_base - j0;
+                    if (lane < n_run && q > 0 && q < kWave)
+                        marks[q] = 1;
+                    // other lanes' marks: the compiler must not forward the lane's own stores
+                    // (one wave: its LDS writes complete before its later reads)
+                    asm volatile("" ::: "memory");
+                    const uint64_t m = __ballot(marks[lane] != 0);
+                    const int i0 = __builtin_popcountll(__ballot(lane < n_run && sp_base <= j0)) - 1;
+                    i = __shfl(i0 + __builtin_popcountll(m & (~0ull >> (63 - lane))), min(lane, nchunk - 1), kWave);
+                }
+            }
+            const int o = j0 + min(lane, nchunk - 1) - __shfl(sp_base, i, kWave);
+            const int nt = __shfl(sp_nt, i, kWave);
+            tile_lane = __shfl(sp_tf, i, kWave) + min(o, nt - 1);
+            mask_lane = o < nt ? tile_lane : -(1 << 24);  // padding: no valid token
+        } else {
             const int p = j0 + min(lane, nchunk - 1);
             int base = 0;
             tile_lane = 0;
@@ -1607,11 +1647,13 @@ void stage1_xdl_kernel(
                 base += split_stop(s);
             }
         }
+        const int bidx = (16 * tile_lane) >> block_size_log2;
+        const bool guessed = j0 == 0 && b == guess_b &&
+                             __ballot(bidx != min(guess_first + lane, max_blocks - 1)) == 0;
+        return guessed ? bt_guess : bt[bidx];
+    };
+    auto chunk_addresses = [&](int blk) {
         {
-            const int bidx = (16 * tile_lane) >> block_size_log2;
-            const bool guessed = j0 == 0 && b == guess_b &&
-                                 __ballot(bidx != min(guess_first + lane, max_blocks - 1)) == 0;
-            const int blk = guessed ? bt_guess : bt[bidx];
             const int toff = (16 * tile_lane) & (block_size - 1);
             // the piece's first record: token toff of kv-head 0 (AoS: at toff * slot_pos)
             const int piece = LAYOUT == 0 ? toff * num_kv_heads * rec : toff * slot_pos;
@@ -1621,11 +1663,30 @@ void stage1_xdl_kernel(
             base_hi = (uint32_t)(a >> 32);
             moff_lane = (block_size - toff) * num_kv_heads * rec + toff * 2;
         }
+    };
+    auto open_chunk = [&](int j0, int nchunk, int last, int nslots) {
+        chunk_addresses(chunk_tiles(j0, nchunk));
         issue_slots(j0, last, 0, nslots);
     };
 
-    // The first chunk's first loads go out before the K table and the q operands are built.
-    open_chunk(0, min(64, total), min(64, total) - 1, FIRST_SLOTS);
+    // The first chunk's first loads go out before the K table and the q operands are built,
+    // and the q (or rotation) loads between its block-table read and those: loads complete in
+    // issue order, so the first KV addresses wait for the block table alone and the q rows
+    // arrive under the first KV loads.
+    const int blk0 = chunk_tiles(0, min(64, total));
+    float4 q_rows[8];
+    RotRows<G> rot_rows;
+    RotCols rot_cols;
+    const int nvh = ROT ? (int)(blockDim.x / kWave) : 1;
+    if constexpr (ROT) {
+        rot_load_rows<QueryT, G>(rot_rows, static_cast<const QueryT *>(query), (int64_t)b * num_q_heads,
+                                 num_q_heads, lane & 15, lane >> 4);
+        rot_load_cols(rot_cols, rot_t, threadIdx.x / kWave, lane & 15, lane >> 4);
+    } else {
+        load_q_rows(q_rows, q_rot, (int64_t)b * num_q_heads + hb + hl, lane >> 4, KF8);
+    }
+    chunk_addresses(blk0);
+    issue_slots(0, min(64, total) - 1, 0, FIRST_SLOTS);
     if constexpr (ROT) {
         // the sequence's rotated queries into qbuf (column tiles w, w + nvh, ... of this wave)
         half8 ah[G / 2][4];
