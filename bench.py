@@ -33,6 +33,10 @@ import time
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "turboquant-cuda-decode_amd"))
+# Kernel arguments in device memory (HIP reads this when it starts, before torch is
+# imported below): with them in host memory every wave's first argument read crosses PCIe
+# and a Stage1 launch at the headline shape takes ~1.6 us longer.
+os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
 
 METRIC = ("Stage1 µs + achieved HBM GB/s (% of peak), B64×ctx4096 Qwen3-4B shape, 1 GPU")
 HBM_PEAK_GBS = 8000.0
