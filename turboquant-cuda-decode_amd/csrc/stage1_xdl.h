@@ -501,6 +501,14 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
 // equally busy; equal lengths give every sequence nw waves (taken without the arithmetic);
 // batches of at most 64 sequences also pair heavy runs with light ones on each SIMD
 // (deal_ranked).
+// a / b for a >= 0, b > 0 (uniform): a shift when b is a power of two, as split counts,
+// split lengths and waves per sequence usually are, else the division
+__device__ __forceinline__ int div_pos(int a, int b) {
+    if ((b & (b - 1)) == 0)
+        return a >> __builtin_ctz((unsigned)b);
+    return a / b;
+}
+
 struct Deal {
     int b, wid, nw;  // b < 0: the deal leaves this wave without work
     int len;         // seq_lens[b], as the deal read it
@@ -1396,11 +1404,11 @@ void stage1_xdl_kernel(
     }
     const int seq_len = FUSED ? seq_lens[b] : dealt_len;
     // split partition: L = ceil(len / S); live splits are those with s * L < len
-    const int split_len = (seq_len + num_splits - 1) / num_splits;
-    const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
+    const int split_len = div_pos(max(seq_len, 0) + num_splits - 1, num_splits);
+    const int live = split_len > 0 ? min(num_splits, div_pos(seq_len + split_len - 1, split_len)) : 0;
     // run x of the W runs of this (sequence, kv-head): live splits from x q + min(x, r), q + 1 of
     // them for x < r and q after (q = live / W, r = live % W)
-    const int run_q = live / run_waves, run_r = live % run_waves;
+    const int run_q = div_pos(live, run_waves), run_r = live - run_q * run_waves;
     const int s_lo = wid * run_q + min(wid, run_r);
     const int s_hi = s_lo + run_q + (wid < run_r ? 1 : 0);
     if constexpr (FUSED) {
@@ -1468,6 +1476,7 @@ void stage1_xdl_kernel(
     const int n_run = s_hi - s_lo;
     const bool run_in_lanes = n_run <= kWave;
     int sp_tf = 0, sp_nt = 0, sp_base = 0;
+    int e_log2 = -1;  // log2 of the positions of every split of the run when they are one power of two
     int total = 0;
     if (run_in_lanes) {
         const int st0 = (s_lo + min(lane, n_run - 1)) * split_len, en = min(st0 + split_len, seq_len);
@@ -1477,6 +1486,9 @@ void stage1_xdl_kernel(
         const int incl = (int)wave_scan((uint32_t)e);
         sp_base = incl - e;
         total = __builtin_amdgcn_readlane(incl, kWave - 1);
+        const int e0 = __builtin_amdgcn_readfirstlane(e);
+        if (__ballot(lane < n_run && e != e0) == 0 && (e0 & (e0 - 1)) == 0)
+            e_log2 = __builtin_ctz((unsigned)e0);
     } else {
         for (int s = s_lo; s < s_hi; ++s)
             total += (split_tiles(s) + 1) & ~1;
@@ -1609,7 +1621,15 @@ void stage1_xdl_kernel(
     // Lane i: the tile and mask of stream position j0 + i and the block-table entry of that
     // tile (read here; the addresses come from chunk_addresses).
     auto chunk_tiles = [&](int j0, int nchunk) {
-        if (run_in_lanes) {
+        if (run_in_lanes && e_log2 >= 0) {
+            // every split takes 2^e_log2 positions (the tail's go to the last one)
+            const int p = j0 + min(lane, nchunk - 1);
+            const int i = min(p >> e_log2, n_run - 1);
+            const int st0 = (s_lo + i) * split_len, en = min(st0 + split_len, seq_len);
+            const int tf = st0 >> 4, nt = ((en - 1) >> 4) - tf + 1, o = p - (i << e_log2);
+            tile_lane = tf + min(o, nt - 1);
+            mask_lane = o < nt ? tile_lane : -(1 << 24);  // padding: no valid token
+        } else if (run_in_lanes) {
             int i = 0;  // the lane's split, as an index into the run
             if constexpr (!FUSED) {
                 if (n_run > 1) {
