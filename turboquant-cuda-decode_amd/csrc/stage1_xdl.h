@@ -514,18 +514,24 @@ struct Deal {
     int len;         // seq_lens[b], as the deal read it
 };
 
-// Live splits and estimated stream positions of sequence bb (0 past the batch): each
-// split's tiles (one more when it straddles a tile edge), as the stream pads them.
+// Live splits and estimated stream positions of a sequence of len tokens (sequence bb, 0
+// past the batch): each split's tiles (one more when it straddles a tile edge), as the
+// stream pads them.
 struct SeqLoad {
     int live;
     uint32_t est;
     int len;
+    int per;  // estimated positions per split
 };
-__device__ __forceinline__ SeqLoad sequence_load(const int32_t *__restrict__ seq_lens, int B, int S, int bb) {
-    const int len = bb < B ? max(seq_lens[bb], 0) : 0;
-    const int split_len = (len + S - 1) / S;
+__device__ __forceinline__ SeqLoad sequence_load_len(int len, int S) {
+    len = max(len, 0);
+    const int split_len = div_pos(len + S - 1, S);
     const int live = split_len > 0 ? (len + split_len - 1) / split_len : 0;
-    return SeqLoad{live, (uint32_t)live * (uint32_t)(((split_len + 15) >> 4) + 1), len};
+    const int per = ((split_len + 15) >> 4) + 1;
+    return SeqLoad{live, (uint32_t)live * (uint32_t)per, len, per};
+}
+__device__ __forceinline__ SeqLoad sequence_load(const int32_t *__restrict__ seq_lens, int B, int S, int bb) {
+    return sequence_load_len(bb < B ? seq_lens[bb] : 0, S);
 }
 
 // Inclusive prefix sum over the wave's 64 lanes: shifts within each 16-lane row, then the
@@ -563,8 +569,9 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
 // and nw*B - 1 - p: a heavy run shares its SIMD with a light one.  The rank-p wave is found
 // by bisection on its load (lane-wide counts of the waves at least that heavy), then by its
 // place among the waves of exactly that load.  Any x -> p bijection keeps the deal exact.
-__device__ Deal deal_ranked(const int32_t *__restrict__ seq_lens, int B, int S, int nw, int x, int lane) {
-    const SeqLoad q = sequence_load(seq_lens, B, S, lane);
+// lane_len: seq_lens[lane] (0 past the batch), read by the caller.
+__device__ Deal deal_ranked(int lane_len, int B, int S, int nw, int x, int lane) {
+    const SeqLoad q = sequence_load_len(lane_len, S);
     const uint32_t est_total = wave_sum(q.est);
     const int n_live = __builtin_popcountll(__ballot(q.live > 0));
     // spare waves before prefix pre: floor(pre * spare / total) with one fp32 ratio -- monotone
@@ -573,8 +580,20 @@ __device__ Deal deal_ranked(const int32_t *__restrict__ seq_lens, int B, int S, 
     auto cut = [&](uint32_t pre) { return (int)floorf((float)pre * ratio); };
     const uint32_t est_out = wave_scan(q.est);
     const int k = q.live > 0 ? min(1 + cut(est_out) - cut(est_out - q.est), q.live) : 0;
-    const int per = q.live > 0 ? (int)(q.est / (uint32_t)q.live) : 0;  // positions per split
-    const int qd = k > 0 ? q.live / k : 0, r = k > 0 ? q.live % k : 0;
+    const int per = q.live > 0 ? q.per : 0;  // positions per split
+    // live / k and live % k (both below 2^16): an fp32 quotient corrected by one step
+    int qd = 0, r = 0;
+    if (k > 0) {
+        qd = (int)((float)q.live * __builtin_amdgcn_rcpf((float)k));
+        r = q.live - qd * k;
+        if (r < 0) {
+            --qd;
+            r += k;
+        } else if (r >= k) {
+            ++qd;
+            r -= k;
+        }
+    }
     const uint32_t l_hi = (uint32_t)((qd + 1) * per), l_lo = (uint32_t)(qd * per);
     const int n_hi = r, n_lo = k - r;  // runs of qd + 1 and of qd splits
     const int T = nw * B;
@@ -608,15 +627,19 @@ __device__ Deal deal_waves(const int32_t *__restrict__ seq_lens, int B, int S, i
     // equal lengths: every sequence keeps its nw waves, as the deal would give them
     const int len0 = seq_lens[0];
     bool equal = true;
+    int lane_len = 0;  // seq_lens[lane] (0 past the batch): the first 64 lengths, read once
     for (int c0 = 0; c0 < B; c0 += kWave) {
         const int bb = c0 + lane;
-        equal = equal && __ballot(bb < B && seq_lens[bb] != len0) == 0;
+        const int len = bb < B ? seq_lens[bb] : len0;
+        if (c0 == 0)
+            lane_len = bb < B ? len : 0;
+        equal = equal && __ballot(len != len0) == 0;
     }
     if (equal)
         return Deal{x / nw, x % nw, nw, len0};
     if (B <= kWave)
-        return deal_ranked(seq_lens, B, S, nw, x, lane);
-    const SeqLoad first = sequence_load(seq_lens, B, S, lane);
+        return deal_ranked(lane_len, B, S, nw, x, lane);
+    const SeqLoad first = sequence_load_len(lane_len, S);
     uint32_t est_total = 0;
     int n_live = 0;
     for (int c0 = 0; c0 < B; c0 += kWave) {
