@@ -24,7 +24,7 @@
  *   block_table int32   [B, max_blocks_per_seq]
  *   seq_lens    int32   [B]
  *   pair_lut    float32 [256, 2]              row lo*16+hi = (c[lo], c[hi])
- *   mid_o       float32 [B, Hq, S, D + 1]     S = num_kv_splits; [.., D] holds LSE
+ *   mid_o       float32 [B, Hq, S, D + 1]     S = num_kv_splits (1 .. 65536); [.., D] holds LSE
  *   out         [B, Hq, D] in out_dtype; lse float32 [B, Hq]
  */
 #ifndef TQ4_DECODE_H

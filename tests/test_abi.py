@@ -48,6 +48,7 @@ def _stage1_call(**over):
     (dict(B=0), 1, "must be positive"),
     (dict(Hq=30), 1, "multiple of Hk"),
     (dict(D=64), 2, "head_dim 64"),
+    (dict(S=65537), 2, "num_kv_splits 65537"),
     (dict(layout=3), 1, "layout"),
     (dict(stride=100), 1, "requires cache"),
     (dict(cache=(1 << 12) + 2), 1, "16-byte aligned"),

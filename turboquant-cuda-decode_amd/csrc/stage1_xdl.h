@@ -581,7 +581,8 @@ __device__ Deal deal_ranked(int lane_len, int B, int S, int nw, int x, int lane)
     const uint32_t est_out = wave_scan(q.est);
     const int k = q.live > 0 ? min(1 + cut(est_out) - cut(est_out - q.est), q.live) : 0;
     const int per = q.live > 0 ? q.per : 0;  // positions per split
-    // live / k and live % k (both below 2^16): an fp32 quotient corrected by one step
+    // live / k and live % k: an fp32 quotient is within 1 of it for live below 2^22 (live <= S),
+    // so one correction step makes it exact
     int qd = 0, r = 0;
     if (k > 0) {
         qd = (int)((float)q.live * __builtin_amdgcn_rcpf((float)k));

@@ -137,6 +137,8 @@ int check_stage1(Stage1Args &a) {
                                    "max_blocks_per_seq must be positive");
     if (a.Hq % a.Hk)
         return fail(TQ4_E_INVALID, "tq4_stage1: Hq (%d) must be a multiple of Hk (%d)", a.Hq, a.Hk);
+    if (a.S > 65536)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: num_kv_splits %d above 65536", a.S);
     if (a.D != tq4::kHeadDim)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: head_dim %d unsupported (kernels are built for 128)", a.D);
     if (!layout_valid(a.layout))
