@@ -3,8 +3,8 @@
 The float32 bits of ``get_centroids(d, bits)`` (``reference/centroids.py:82-86``) are
 the one output on this path that no closed form or invariant fixes exactly, so
 this script imports that pure-Python function from the reference checkout (read
-only) in the build container and records its output.  The GPU box never runs
-this script; it only reads the JSON it wrote.
+only) where the reference checkout is present and records its output.  The tests
+never run this script; they only read the JSON it wrote.
 
 Usage: ``python tests/golden/make_centroids_golden.py [/root/reference]``
 """
