@@ -529,7 +529,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # a process's first ~40 cold launches run 1-3 us slow (63-65 us, then 62); 100 untimed
+    # launches put the timed ones in the steady state
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layout", default="soa", choices=["soa", "aos"])
     ap.add_argument("--slots", default="random", choices=["random", "contiguous"],
                     help="writer workloads: token slots scattered over the pool, or in order")
@@ -582,12 +584,14 @@ def main() -> int:
 
     def cold_times(layout, kernel, steps, warmup, stamped=True):
         """Durations (ms) of `steps` cold launches: the kernel's own start/end stamps, or
-        (stamped=False) events recorded around each launch."""
+        (stamped=False) events recorded around each launch.  The events are created before
+        the warm-up, so the GPU does not sit idle (and clock down) between the warm-up and
+        the timed launches."""
+        ev = [timer.pair() for _ in range(steps)]
         for _ in range(warmup):
             flush.sum()
             launch(layout, kernel)
         torch.cuda.synchronize()
-        ev = [timer.pair() for _ in range(steps)]
         for a, b in ev:
             flush.sum()  # 1 GiB read sweep: evicts L2 and the Infinity Cache
             if stamped:
