@@ -41,6 +41,9 @@ os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
 METRIC = ("Stage1 µs + achieved HBM GB/s (% of peak), B64×ctx4096 Qwen3-4B shape, 1 GPU")
 HBM_PEAK_GBS = 8000.0
 FLUSH_BYTES = 1 << 30
+# untimed launches before each side workload's timed ones: a process's first launches on
+# new buffers run 1-3 us slow (the Stage1 headline: ~40 of them)
+SIDE_WARMUP = 40
 PROFILES = ROOT / "profiles"
 
 
@@ -165,7 +168,7 @@ def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4), slots_mode="
         else:
             slots = torch.randperm(n_blocks * 16, device=dev)[:n_tok].to(torch.int32)
         times = []
-        for i in range(reps + 3):
+        for i in range(reps + SIDE_WARMUP):
             flush.sum()
             a, b = timer.pair()
             timer.stamp_next_launch(a, b)  # the kernel's own start and end
@@ -174,7 +177,7 @@ def store_times(dev, flush, timer, reps=30, only=None, bits=(4, 4), slots_mode="
             else:
                 ops.store_preset(key, val, cache, slots, rot, m, c, key_bits=kb, value_bits=vb)
             torch.cuda.synchronize()
-            if i >= 3:
+            if i >= SIDE_WARMUP:
                 times.append(timer.elapsed_ms(a, b) * 1e3)
             timer.destroy(a, b)
         us = statistics.median(times)
@@ -200,14 +203,14 @@ def full_decode_time(dev, flush, timer, reps=30):
             t(w.centroids), w.num_kv_splits)
     ws = ops.DecodeWorkspace(w.batch, w.num_q_heads, w.num_kv_splits, dev, torch.float16)
     times = []
-    for i in range(reps + 3):
+    for i in range(reps + SIDE_WARMUP):
         flush.sum()
         a, b = timer.pair()
         timer.record(a)
         ops.full_decode(*args, workspace=ws)
         timer.record(b)
         torch.cuda.synchronize()
-        if i >= 3:
+        if i >= SIDE_WARMUP:
             times.append(timer.elapsed_ms(a, b) * 1e3)
         timer.destroy(a, b)
     us = statistics.median(times)
@@ -270,7 +273,7 @@ def stage1_preset_time(dev, flush, timer, name, reps=30, l2_resident=False):
         run = lambda: ops.stage1_preset(q, c, bt, sl, cents, mid, key_bits=preset[0],  # noqa: E731
                                         value_bits=preset[1])
     times = []
-    for i in range(reps + 3):
+    for i in range(reps + SIDE_WARMUP):
         if l2_resident:
             run()
         else:
@@ -279,7 +282,7 @@ def stage1_preset_time(dev, flush, timer, name, reps=30, l2_resident=False):
         timer.stamp_next_launch(a, b)
         run()
         torch.cuda.synchronize()
-        if i >= 3:
+        if i >= SIDE_WARMUP:
             times.append(timer.elapsed_ms(a, b) * 1e3)
         timer.destroy(a, b)
     us = statistics.median(times)
@@ -300,13 +303,13 @@ def stage1_workload_time(dev, flush, timer, w, reps=30, kernel="auto"):
     q, c, bt, sl, lut = t(w.q_rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens), t(w.pair_lut)
     mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
     times = []
-    for i in range(reps + 3):
+    for i in range(reps + SIDE_WARMUP):
         flush.sum()
         a, b = timer.pair()
         timer.stamp_next_launch(a, b)
         ops.stage1(q, c, bt, sl, lut, mid, kernel=kernel)
         torch.cuda.synchronize()
-        if i >= 3:
+        if i >= SIDE_WARMUP:
             times.append(timer.elapsed_ms(a, b) * 1e3)
         timer.destroy(a, b)
     us = statistics.median(times)
@@ -328,13 +331,13 @@ def stage2_time(dev, flush, timer, w, mid, reps=30):
     out = torch.empty(w.batch, w.num_q_heads, w.head_dim, device=dev)
     lse = torch.empty(w.batch, w.num_q_heads, device=dev)
     times = []
-    for i in range(reps + 3):
+    for i in range(reps + SIDE_WARMUP):
         flush.sum()
         a, b = timer.pair()
         timer.stamp_next_launch(a, b)
         ops.stage2(mid, sl, out, lse)
         torch.cuda.synchronize()
-        if i >= 3:
+        if i >= SIDE_WARMUP:
             times.append(timer.elapsed_ms(a, b) * 1e3)
         timer.destroy(a, b)
     us = statistics.median(times)
@@ -479,13 +482,13 @@ def side_workload(args, dev) -> int:
         bt16 = (torch.arange(w.block_table.shape[1], dtype=torch.int32, device=dev) % 16).repeat(w.batch, 1)
         mid = torch.empty(w.batch, w.num_q_heads, w.num_kv_splits, w.head_dim + 1, device=dev)
         times = []
-        for i in range(args.steps + 3):
+        for i in range(args.steps + SIDE_WARMUP):
             ops.stage1(q, c, bt16, sl, lut, mid, layout=args.layout)  # warms L2 with the 16 blocks
             a, b = timer.pair()
             timer.stamp_next_launch(a, b)
             ops.stage1(q, c, bt16, sl, lut, mid, layout=args.layout)
             torch.cuda.synchronize()
-            if i >= 3:
+            if i >= SIDE_WARMUP:
                 times.append(timer.elapsed_ms(a, b) * 1e3)
             timer.destroy(a, b)
         us = round(statistics.median(times), 2)
