@@ -491,6 +491,14 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
     return r;
 }
 
+// a / b for a >= 0, b > 0 (uniform): a shift when b is a power of two, as split counts,
+// split lengths and waves per sequence usually are, else the division
+__device__ __forceinline__ int div_pos(int a, int b) {
+    if ((b & (b - 1)) == 0)
+        return a >> __builtin_ctz((unsigned)b);
+    return a / b;
+}
+
 // Waves of one kv-head dealt to the sequences.  The grid gives every kv-head nw * B
 // waves (wave x = wid + nw * b), a number fixed by the shapes alone.  A sequence with live
 // splits gets one wave plus a share of the other nw * B - n_live in proportion to its
@@ -501,14 +509,6 @@ __device__ __forceinline__ TileV decode_v(const RawV<LAYOUT, TPL> &t, const Lane
 // equally busy; equal lengths give every sequence nw waves (taken without the arithmetic);
 // batches of at most 64 sequences also pair heavy runs with light ones on each SIMD
 // (deal_ranked).
-// a / b for a >= 0, b > 0 (uniform): a shift when b is a power of two, as split counts,
-// split lengths and waves per sequence usually are, else the division
-__device__ __forceinline__ int div_pos(int a, int b) {
-    if ((b & (b - 1)) == 0)
-        return a >> __builtin_ctz((unsigned)b);
-    return a / b;
-}
-
 struct Deal {
     int b, wid, nw;  // b < 0: the deal leaves this wave without work
     int len;         // seq_lens[b], as the deal read it
