@@ -4,7 +4,8 @@ that combinations no hand-written case covers meet the oracle.
 
 Bar: max-abs <= 1e-4 on mid_o (outputs and LSE, fp32) and the same untouched-split pattern
 (NaN-prefilled; empty splits stay NaN), for the auto kernel and, where it has an instance
-for the group, the VALU kernel.
+for the group, the VALU kernel; and the same for the FP8-key and 3-bit presets (caches
+written by the oracle writers).
 """
 import numpy as np
 import pytest
@@ -68,3 +69,74 @@ def test_random_shape_matches_oracle(dev, c):
         err = np.nanmax(np.abs(got - ref)) if np.isfinite(ref).any() else 0.0
         print(f"{_id(c)} {kernel}: max-abs {err:.3e}")
         assert err <= TOL, f"{kernel}: max-abs {err} > {TOL}"
+
+
+# The presets (3-bit K with 4- or 3-bit V, FP8 keys) over seeded random shapes, smaller
+# (their oracle is the float64 numpy restatement).
+def _preset_case(i):
+    rng = np.random.default_rng(20261302 + i)
+    preset = [(3, 4), (3, 3), "fp8"][i % 3]
+    hk = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([g for g in (1, 2, 3, 4, 6, 8, 16) if hk * g <= 64]))
+    batch = int(rng.integers(1, 25))
+    splits = int(rng.choice([1, 3, 8, 16, 32]))
+    bs = int(rng.choice([16, 16, 32]))
+    layout = str(rng.choice(["soa", "aos"]))
+    kind = rng.random(batch)
+    lens = np.where(kind < 0.15, 0, np.where(kind < 0.3, rng.integers(1, 40, batch),
+                                             rng.integers(40, 900, batch)))
+    while lens.sum() * hk > 60_000:
+        lens = lens // 2
+    return dict(seed=20261302 + i, preset=preset, hk=hk, group=group, batch=batch, splits=splits,
+                bs=bs, layout=layout, lens=lens.astype(np.int32))
+
+
+PRESET_CASES = [_preset_case(i) for i in range(24)]
+
+
+def _pid(c):
+    name = "fp8" if c["preset"] == "fp8" else "k%dv%d" % c["preset"]
+    return f"{name}-B{c['batch']}-hk{c['hk']}-g{c['group']}-S{c['splits']}-bs{c['bs']}-{c['layout']}"
+
+
+@pytest.mark.parametrize("c", PRESET_CASES, ids=[_pid(c) for c in PRESET_CASES])
+def test_random_shape_preset_matches_oracle(dev, c):
+    from oracle import bits as obits
+    from oracle import fp8 as ofp8
+    from oracle import stage1 as ostage
+    from oracle import store as ostore
+    from tq4_decode import codebook
+
+    rng = np.random.default_rng(c["seed"])
+    hk, bs, layout, lens = c["hk"], c["bs"], c["layout"], c["lens"]
+    aos = layout == "aos"
+    w = workloads.small(c["seed"], c["batch"], lens, c["splits"], num_q_heads=hk * c["group"],
+                        num_kv_heads=hk, block_size=bs)
+    nb = w.kv_cache.shape[0]
+    key = rng.standard_normal((nb * bs, hk, 128)).astype(np.float32)
+    value = (rng.standard_normal((nb * bs, hk, 128)) * 0.8).astype(np.float32)
+    q = rng.standard_normal((c["batch"], hk * c["group"], 128)).astype(np.float32)
+    mid = torch.full((c["batch"], hk * c["group"], c["splits"], 129), float("nan"), device=dev)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    if c["preset"] == "fp8":
+        cache = np.zeros((nb, bs, hk, ofp8.slot_bytes(128)), np.uint8)
+        ostore.store_fp8(key, value, np.arange(nb * bs, dtype=np.int32), cache, block_size=bs, is_aos=aos)
+        ops.stage1_fp8(t(q), t(cache), t(w.block_table), t(w.seq_lens), mid, layout=layout)
+        ref = ostage.stage1(q, cache, w.block_table, w.seq_lens, None, c["splits"], num_kv_heads=hk,
+                            block_size=bs, is_aos=aos, key_fp8=True)
+    else:
+        kb, vb = c["preset"]
+        cents = codebook.centroids(128, kb).astype(np.float32)
+        cache = np.zeros((nb, bs, hk, obits.slot_bytes(128, kb, vb)), np.uint8)
+        obits.store(key, value, np.arange(nb * bs), workloads.random_orthogonal(rng, 128), cents, cache,
+                    kb, vb, block_size=bs, is_aos=aos)
+        ops.stage1_preset(t(q), t(cache), t(w.block_table), t(w.seq_lens), t(cents), mid, key_bits=kb,
+                          value_bits=vb, layout=layout)
+        ref = ostage.stage1(q, cache, w.block_table, w.seq_lens, cents, c["splits"], num_kv_heads=hk,
+                            block_size=bs, is_aos=aos, bits=(kb, vb))
+    torch.cuda.synchronize()
+    got = mid.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "untouched-split pattern differs"
+    err = np.nanmax(np.abs(got - ref)) if np.isfinite(ref).any() else 0.0
+    print(f"{_pid(c)}: max-abs {err:.3e}")
+    assert err <= TOL, f"max-abs {err} > {TOL}"
