@@ -15,8 +15,10 @@ template <typename T> __device__ __forceinline__ float to_float(T x) { return (f
 // are merged 32 at a time in one pass: lane i reads split i's LSE while every lane reads its
 // two dims of all 32 rows (buffer loads at any 4-byte offset: the 516-byte rows are not
 // 8-byte aligned), so a wave has its whole share of mid_o in flight at once; then the
-// weights exp(lse_s - max) are broadcast lane by lane.  A later chunk (more than 32 splits)
-// rescales what came before to its own max.
+// weights exp(lse_s - max) are broadcast lane by lane.  The first chunk's rows are requested
+// before the sequence's length arrives (rows past the non-empty splits, never written, are
+// replaced by zeros and weight 0), so the length's latency hides under theirs.  A later
+// chunk (more than 32 splits) rescales what came before to its own max.
 constexpr int kMergeRows = 32;
 template <typename OutT>
 __global__ __launch_bounds__(kWave) void stage2_kernel(const float *__restrict__ mid_o,
@@ -27,31 +29,45 @@ __global__ __launch_bounds__(kWave) void stage2_kernel(const float *__restrict__
     const int h = blockIdx.x;
     const int b = blockIdx.y;
     const int lane = threadIdx.x;
-    const int seq_len = seq_lens[b];
-    const int split_len = (seq_len + num_splits - 1) / num_splits;
-    // splits [0, live) are the non-empty ones: split s is non-empty iff s * len < seq_len
-    const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
     constexpr int kRow = (kHeadDim + 1) * 4;  // bytes per split row
     const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(mid_o + ((int64_t)b * num_q_heads + h) * num_splits * (kHeadDim + 1)), 0, 0x7FFFFFFF,
         0x00020000);
-
-    float mx = -INFINITY, a0 = 0.f, a1 = 0.f, wsum = 0.f;
-    for (int s0 = 0; s0 < live; s0 += kMergeRows) {
-        const int n = min(kMergeRows, live - s0);
-        const float l = lane < n ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                                  rows, (s0 + lane) * kRow + kHeadDim * 4, 0, 0))
-                                 : -INFINITY;
-        // rows past the chunk re-read its last row (a cache hit); their weight is 0
-        float v0[kMergeRows], v1[kMergeRows];
+    // rows s0 .. s0 + 31 (rows past the last one, n_rows, re-read it: a cache hit)
+    float l, v0[kMergeRows], v1[kMergeRows];
+    auto load_chunk = [&](int s0, int n_rows) {
+        l = lane < n_rows ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                           rows, (s0 + lane) * kRow + kHeadDim * 4, 0, 0))
+                          : -INFINITY;
 #pragma unroll
         for (int i = 0; i < kMergeRows; ++i) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rows, (s0 + min(i, n - 1)) * kRow + 8 * lane, 0, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rows, (s0 + min(i, n_rows - 1)) * kRow + 8 * lane, 0, 0);
             // (elements copied out first: a bit cast applied to an element of the vector
             // in place reads element 0)
             const uint32_t x0 = v[0], x1 = v[1];
             v0[i] = __builtin_bit_cast(float, x0);
             v1[i] = __builtin_bit_cast(float, x1);
+        }
+    };
+    load_chunk(0, min(kMergeRows, num_splits));
+    const int seq_len = seq_lens[b];
+    const int split_len = (seq_len + num_splits - 1) / num_splits;
+    // splits [0, live) are the non-empty ones: split s is non-empty iff s * len < seq_len
+    const int live = split_len > 0 ? min(num_splits, (seq_len + split_len - 1) / split_len) : 0;
+
+    float mx = -INFINITY, a0 = 0.f, a1 = 0.f, wsum = 0.f;
+    for (int s0 = 0; s0 < live; s0 += kMergeRows) {
+        const int n = min(kMergeRows, live - s0);
+        if (s0 > 0) {
+            load_chunk(s0, n);
+        } else {
+            // the first chunk was loaded for all of its splits: drop the empty ones
+            l = lane < n ? l : -INFINITY;
+#pragma unroll
+            for (int i = 0; i < kMergeRows; ++i) {
+                v0[i] = i < n ? v0[i] : 0.f;
+                v1[i] = i < n ? v1[i] : 0.f;
+            }
         }
         const float m_new = fmaxf(mx, wave_max(l));
         const float scale = expf(mx - m_new);  // 0 for the first chunk (mx = -inf)
