@@ -1300,9 +1300,10 @@ __device__ __forceinline__ void rot_column_tile(const half8 (&ah)[G / 2][4], con
 }
 
 // One wave handles a run of consecutive live splits of one (sequence, kv-head).  Their
-// tiles form one stream: split s contributes n_s tiles padded to a multiple of 4 stream
-// positions (padding positions re-read the split's last tile and mask every token), so
-// split ends fall on 4-stage boundaries (after an odd stage's PV).  After a split's last
+// tiles form one stream: split s contributes its n_s tiles padded to an even count, the
+// wave's last split as many more as make the stream whole ring turns (padding positions
+// re-read the split's last tile and mask every token), so split ends fall after an odd
+// stage, with the PV of the split's last pair of positions.  After a split's last
 // stage the wave puts its rows into the LDS image (flushed to mid_o when full and after
 // the wave's last split) and restarts the softmax state and the accumulators.
 //
