@@ -11,7 +11,7 @@
  * message readable with tq4_last_error() on the calling thread.  Nothing throws.
  *
  * Shapes (row-major, contiguous):
- *   q_rot       float32 [B, Hq, D]            (D == 128)
+ *   q_rot       float32 [B, Hq, D]            (D == 128; B = batch, 1 .. 65535)
  *   kv_cache    uint8   [num_blocks, block_size, Hk, slot]  slot = 134 at D=128,
  *               physical block stride = cache_block_stride bytes.  Inside a block, SoA
  *               has its own layout; an AoS slot (t, h) starts at (t*Hk + h)*slot

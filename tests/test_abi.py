@@ -49,6 +49,7 @@ def _stage1_call(**over):
     (dict(Hq=30), 1, "multiple of Hk"),
     (dict(D=64), 2, "head_dim 64"),
     (dict(S=65537), 2, "num_kv_splits 65537"),
+    (dict(B=65536), 2, "batch 65536"),
     (dict(layout=3), 1, "layout"),
     (dict(stride=100), 1, "requires cache"),
     (dict(cache=(1 << 12) + 2), 1, "16-byte aligned"),
@@ -64,6 +65,9 @@ def test_stage2_and_helpers_reject_bad_arguments():
     assert lib.tq4_stage2(None, 1, 1, 0, 1, 1, 1, 128, 4, None) == 1
     assert lib.tq4_stage2(8, 8, 8, 7, 8, 1, 1, 128, 4, None) == 1
     assert "out_dtype" in lib.tq4_last_error().decode()
+    assert lib.tq4_stage2(8, 8, 8, 0, 8, 1, 1, 128, 65537, None) == 2
+    assert lib.tq4_stage2(8, 8, 8, 0, 8, 65536, 1, 128, 4, None) == 2
+    assert "above 65535" in lib.tq4_last_error().decode()
     assert lib.tq4_rotate_query(8, 0, 8, 8, 4, 64, None) == 2
     assert lib.tq4_build_pair_lut(8, 8, 8, None) == 2
 

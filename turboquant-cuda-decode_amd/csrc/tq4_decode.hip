@@ -139,6 +139,8 @@ int check_stage1(Stage1Args &a) {
         return fail(TQ4_E_INVALID, "tq4_stage1: Hq (%d) must be a multiple of Hk (%d)", a.Hq, a.Hk);
     if (a.S > 65536)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: num_kv_splits %d above 65536", a.S);
+    if (a.B > 65535)  // a grid dimension
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: batch %d above 65535", a.B);
     if (a.D != tq4::kHeadDim)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage1: head_dim %d unsupported (kernels are built for 128)", a.D);
     if (!layout_valid(a.layout))
@@ -539,6 +541,9 @@ int tq4_stage2(const float *mid_o, const int32_t *seq_lens, void *out, int out_d
         return fail(TQ4_E_INVALID, "tq4_stage2: B, Hq and num_kv_splits must be positive");
     if (D != tq4::kHeadDim)
         return fail(TQ4_E_UNSUPPORTED, "tq4_stage2: head_dim %d unsupported (128)", D);
+    if (num_kv_splits > 65536 || B > 65535)
+        return fail(TQ4_E_UNSUPPORTED, "tq4_stage2: num_kv_splits %d above 65536 or batch %d above 65535",
+                    num_kv_splits, B);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const dim3 grid(Hq, B);
     switch (out_dtype) {
