@@ -41,7 +41,7 @@ def _case(i):
                 layout=layout, lens=lens.astype(np.int32))
 
 
-CASES = [_case(i) for i in range(48)]
+CASES = [_case(i) for i in range(160)]
 
 
 def _id(c):
@@ -91,7 +91,7 @@ def _preset_case(i):
                 bs=bs, layout=layout, lens=lens.astype(np.int32))
 
 
-PRESET_CASES = [_preset_case(i) for i in range(24)]
+PRESET_CASES = [_preset_case(i) for i in range(72)]
 
 
 def _pid(c):
