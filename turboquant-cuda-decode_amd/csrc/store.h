@@ -369,7 +369,12 @@ __global__ __launch_bounds__(kWave *W) __attribute__((amdgpu_waves_per_eu(W == k
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float v = x[8 * kb + j] * rn;
+                // v as one fp32 register value: otherwise the compiler may fold the product
+                // into one of the f16 casts (v_fma_mix, a single rounding) and not the other, and
+                // where the two roundings differ (the fp32 product on an f16 tie) hi + lo is off
+                // by an f16 ulp of x_hat * 16
+                float v = x[8 * kb + j] * rn;
+                asm("" : "+v"(v));
                 b_hi[kb][j] = (_Float16)v;
                 b_lo[kb][j] = (_Float16)(v - (float)b_hi[kb][j]);
             }
