@@ -4,8 +4,9 @@ that combinations no hand-written case covers meet the oracle.
 
 Bar: max-abs <= 1e-4 on mid_o (outputs and LSE, fp32) and the same untouched-split pattern
 (NaN-prefilled; empty splits stay NaN), for the auto kernel and, where it has an instance
-for the group, the VALU kernel; and the same for the FP8-key and 3-bit presets (caches
-written by the oracle writers).
+for the group, the VALU kernel (AoS cases also through the backend's head-major storage and
+its transpose(1, 2) view); and the same for the FP8-key and 3-bit presets (caches written by
+the oracle writers).
 """
 import numpy as np
 import pytest
@@ -60,9 +61,14 @@ def test_random_shape_matches_oracle(dev, c):
     t = lambda a: to_dev(a, dev)  # noqa: E731
     args = (t(w.q_rot), t(cache), t(w.block_table), t(w.seq_lens), t(w.pair_lut))
     kernels = ["auto"] + (["simple"] if c["group"] in SIMPLE_GROUPS else [])
-    for kernel in kernels:
+    runs = [(kernel, args) for kernel in kernels]
+    if layout == "aos":
+        # the same slots through the backend's head-major storage and its transpose(1, 2) view
+        storage = t(cache).permute(0, 2, 1, 3).contiguous()
+        runs.append(("auto/head-major view", (args[0], storage.transpose(1, 2)) + args[2:]))
+    for kernel, a in runs:
         mid = torch.full((w.batch, w.num_q_heads, w.num_kv_splits, 129), float("nan"), device=dev)
-        ops.stage1(*args, mid, layout=layout, kernel=kernel)
+        ops.stage1(*a, mid, layout=layout, kernel=kernel.split("/")[0])
         torch.cuda.synchronize()
         got = mid.cpu().numpy()
         assert np.array_equal(np.isnan(got), np.isnan(ref)), f"{kernel}: untouched-split pattern differs"
