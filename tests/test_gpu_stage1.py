@@ -89,12 +89,24 @@ def test_gqa_6_and_16_on_the_mfma_kernel(dev, layout, group):
 
 
 @pytest.mark.parametrize("kernel", ["simple", "xdl"])
-@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("bs", [32, 64, 128, 256])
 def test_larger_kv_blocks(dev, kernel, bs):
     w = workloads.small(103, 3, [130, 511, 64], 5, block_size=bs)
     for layout in ("soa", "aos"):
         cache = workloads.soa_to_aos(w.kv_cache, w.centroids, 8, block_size=bs) if layout == "aos" else None
         assert_parity(run(w, dev, kernel, layout, cache), oracle(w, layout, cache))
+
+
+@pytest.mark.parametrize("bs", [8, 48])
+def test_block_sizes_the_mfma_kernel_does_not_take(dev, bs):
+    """Block sizes below 16 or not a power of two: "auto" runs the VALU kernel, and asking for
+    the 16x16x32 kernel is an error, not a wrong result."""
+    w = workloads.small(104, 4, [700, 33, 0, 2000], 8, block_size=bs)
+    for layout in ("soa", "aos"):
+        cache = workloads.soa_to_aos(w.kv_cache, w.centroids, 8, block_size=bs) if layout == "aos" else None
+        assert_parity(run(w, dev, "auto", layout, cache), oracle(w, layout, cache))
+        with pytest.raises(RuntimeError, match="power-of-two block_size"):
+            run(w, dev, "xdl", layout, cache)
 
 
 @pytest.mark.parametrize("kernel", ["simple", "xdl"])
