@@ -199,3 +199,26 @@ def test_stage1_fp8_xdl_larger_blocks(dev, layout, bs):
     ref = ostage.stage1(query, cache, w.block_table, w.seq_lens, None, 8, num_kv_heads=HK,
                         block_size=bs, is_aos=layout == "aos", key_fp8=True)
     _assert_parity(got, ref)
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("bs", [64, 256])
+def test_fp8_larger_kv_blocks(dev, layout, bs):
+    """The 16x16x32 kernel at 64 / 256-token KV blocks (several 16-token pieces per block: the
+    piece and metadata offsets use the 192-byte FP8 record)."""
+    rng = np.random.default_rng(330 + bs)
+    lens = [130, 511, 64, 2000]
+    w = workloads.small(330 + bs, len(lens), lens, 8, num_q_heads=32, num_kv_heads=HK, block_size=bs)
+    nb = w.kv_cache.shape[0]
+    key = (rng.standard_normal((nb * bs, HK, D)) * 2).astype(np.float32)
+    value = rng.standard_normal((nb * bs, HK, D)).astype(np.float32)
+    cache = np.zeros((nb, bs, HK, SLOT), np.uint8)
+    ostore.store_fp8(key, value, np.arange(nb * bs, dtype=np.int32), cache, block_size=bs, is_aos=layout == "aos")
+    query = rng.standard_normal((len(lens), 32, D)).astype(np.float32)
+    mid = torch.full((len(lens), 32, 8, D + 1), float("nan"), device=dev)
+    ops.stage1_fp8(to_dev(query, dev), to_dev(cache, dev), to_dev(w.block_table, dev), to_dev(w.seq_lens, dev),
+                   mid, layout=layout, kernel="xdl")
+    torch.cuda.synchronize()
+    ref = ostage.stage1(query, cache, w.block_table, w.seq_lens, None, 8, num_kv_heads=HK, block_size=bs,
+                        is_aos=layout == "aos", key_fp8=True)
+    _assert_parity(mid.cpu().numpy(), ref)

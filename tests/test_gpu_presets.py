@@ -262,9 +262,9 @@ def test_stage1_k3_on_the_mfma_kernel(dev, layout, group, vb):
 
 @pytest.mark.parametrize("vb", [4, 3])
 @pytest.mark.parametrize("layout", ["soa", "aos"])
-@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("bs", [32, 64, 128, 256])
 def test_stage1_k3_mfma_larger_blocks(dev, layout, bs, vb):
-    """The 16x16x32 kernel at 32 / 64-token KV blocks (several 16-token pieces per block:
+    """The 16x16x32 kernel at 32 - 256-token KV blocks (several 16-token pieces per block:
     the piece and metadata offsets use the preset's record size)."""
     hk = 8
     bt, lens, cache, cents, rng = _preset_cache(470 + bs, [130, 511, 64, 2000], hk, 3, vb, layout, bs=bs)
