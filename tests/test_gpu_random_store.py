@@ -30,7 +30,11 @@ def _case(i):
                 layout=str(rng.choice(["soa", "aos"])), skip=float(rng.choice([0.0, 0.2])))
 
 
-CASES = [_case(i) for i in range(24)]
+CASES = [_case(i) for i in range(24)] + [  # 128- and 256-token KV blocks
+    dict(seed=20261530, hk=8, bs=128, n_tok=700, dtype="bf16", layout="soa", skip=0.2),
+    dict(seed=20261531, hk=2, bs=256, n_tok=1000, dtype="f32", layout="aos", skip=0.0),
+    dict(seed=20261532, hk=4, bs=256, n_tok=333, dtype="f16", layout="soa", skip=0.2),
+    dict(seed=20261533, hk=1, bs=128, n_tok=64, dtype="bf16", layout="aos", skip=0.2)]
 
 
 def _id(c):

@@ -31,7 +31,11 @@ def _case(i):
                 skip=float(rng.choice([0.0, 0.2])))
 
 
-CASES = [_case(i) for i in range(24)]
+CASES = [_case(i) for i in range(24)] + [  # 128- and 256-token KV blocks
+    dict(seed=20261630, preset="fp8", hk=8, bs=256, n_tok=700, dtype="bf16", layout="soa", skip=0.2),
+    dict(seed=20261631, preset=(3, 4), hk=2, bs=128, n_tok=1000, dtype="f32", layout="aos", skip=0.0),
+    dict(seed=20261632, preset=(3, 3), hk=4, bs=256, n_tok=333, dtype="f16", layout="soa", skip=0.2),
+    dict(seed=20261633, preset="fp8", hk=1, bs=128, n_tok=64, dtype="f32", layout="aos", skip=0.2)]
 
 
 def _id(c):
