@@ -222,3 +222,21 @@ def test_fp8_larger_kv_blocks(dev, layout, bs):
     ref = ostage.stage1(query, cache, w.block_table, w.seq_lens, None, 8, num_kv_heads=HK, block_size=bs,
                         is_aos=layout == "aos", key_fp8=True)
     _assert_parity(mid.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("kernel", ["xdl", "simple"])
+def test_fp8_attention_scale(dev, kernel):
+    """A non-default attn_scale (0.03: FP8 keys carry the raw key magnitudes) reaches the scores."""
+    w, cache, query = _fp8_workload(340, [700, 33, 1500, 129], 8)
+    got = np.asarray(_stage1_scaled(dev, w, cache, query, kernel, 0.03))
+    ref = ostage.stage1(query, cache, w.block_table, w.seq_lens, None, 8, num_kv_heads=HK, block_size=BS,
+                        key_fp8=True, attn_scale=0.03)
+    _assert_parity(got, ref)
+
+
+def _stage1_scaled(dev, w, cache, query, kernel, scale):
+    mid = torch.full((w.batch, w.num_q_heads, 8, D + 1), float("nan"), device=dev)
+    ops.stage1_fp8(to_dev(query, dev), to_dev(cache, dev), to_dev(w.block_table, dev), to_dev(w.seq_lens, dev), mid,
+                   layout="soa", kernel=kernel, attn_scale=scale)
+    torch.cuda.synchronize()
+    return mid.cpu().numpy()

@@ -273,3 +273,19 @@ def test_stage1_k3_mfma_larger_blocks(dev, layout, bs, vb):
     ref = ostage.stage1(q, cache, bt, lens, cents, 8, num_kv_heads=hk, block_size=bs,
                         is_aos=layout == "aos", bits=(3, vb))
     _assert_parity(got, ref)
+
+
+@pytest.mark.parametrize("preset", PRESETS)
+@pytest.mark.parametrize("kernel", ["xdl", "simple"])
+def test_stage1_preset_attention_scale(dev, preset, kernel):
+    """A non-default attn_scale (0.3 instead of 1 / sqrt(D)) reaches the scores of the presets."""
+    kb, vb = preset
+    hk = 8
+    bt, lens, cache, cents, rng = _preset_cache(480 + vb, [700, 33, 1500, 129], hk, kb, vb, "soa")
+    q = rng.standard_normal((len(lens), hk * 4, D)).astype(np.float32)
+    mid = torch.full((len(lens), hk * 4, 8, D + 1), float("nan"), device=dev)
+    ops.stage1_preset(to_dev(q, dev), to_dev(cache, dev), to_dev(bt, dev), to_dev(lens, dev), to_dev(cents, dev), mid,
+                      key_bits=kb, value_bits=vb, layout="soa", attn_scale=0.3, kernel=kernel)
+    torch.cuda.synchronize()
+    ref = ostage.stage1(q, cache, bt, lens, cents, 8, num_kv_heads=hk, block_size=BS, bits=(kb, vb), attn_scale=0.3)
+    _assert_parity(mid.cpu().numpy(), ref)

@@ -354,3 +354,20 @@ def test_retired_kernel_id_is_rejected(dev):
     torch.cuda.synchronize()
     assert rc == 2 and b"retired" in lib.tq4_last_error()
     assert torch.isnan(mid).all()
+
+
+@pytest.mark.parametrize("kernel", ["xdl", "simple"])
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+@pytest.mark.parametrize("scale", [0.01, 0.3, 2.0])
+def test_attention_scales(dev, kernel, layout, scale):
+    """Scores scale with attn_scale (the default is 1 / sqrt(D)); at 2.0 the scores reach tens of
+    units, so the max rescale path runs too."""
+    w = workloads.small(120, 4, [700, 33, 1500, 129], 8)
+    cache = workloads.soa_to_aos(w.kv_cache, w.centroids, 8) if layout == "aos" else w.kv_cache
+    mid = torch.full((w.batch, w.num_q_heads, w.num_kv_splits, 129), float("nan"), device=dev)
+    ops.stage1(to_dev(w.q_rot, dev), to_dev(cache, dev), to_dev(w.block_table, dev), to_dev(w.seq_lens, dev),
+               to_dev(w.pair_lut, dev), mid, layout=layout, kernel=kernel, attn_scale=scale)
+    torch.cuda.synchronize()
+    ref = native.stage1(w.q_rot, cache, w.block_table, w.seq_lens, w.centroids, w.num_kv_splits,
+                        num_kv_heads=8, block_size=16, is_aos=layout == "aos", attn_scale=scale)
+    assert_parity(mid.cpu().numpy(), ref)
