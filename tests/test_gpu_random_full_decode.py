@@ -79,3 +79,25 @@ def test_full_decode_random_shape(dev, c):
         print(f"out excess {err_o.max():.3e}, lse max-abs {err_l:.3e}")
         assert err_o.max() <= 2e-4
         assert err_l <= 2e-4
+
+
+@pytest.mark.parametrize("batch", [4, 256])
+def test_full_decode_attention_scale(dev, batch):
+    """A non-default attn_scale through both paths: the four-launch step (batch 4) and the one
+    launch with the rotation inside Stage1 (batch 256, one wave per sequence and kv-head)."""
+    rng = np.random.default_rng(20261499 + batch)
+    lens = rng.integers(1, 900, batch).astype(np.int32)
+    w = workloads.small(20261499 + batch, batch, lens, 16, num_q_heads=32, num_kv_heads=8)
+    query = torch.from_numpy(rng.standard_normal((batch, 32, 128)).astype(np.float32)).to(torch.float16)
+    rot = workloads.random_orthogonal(rng, 128)
+    t = lambda a: to_dev(a, dev)  # noqa: E731
+    out, lse = ops.full_decode(query.to(dev), t(rot), t(w.kv_cache), t(w.block_table), t(w.seq_lens),
+                               t(w.centroids), 16, out_dtype=torch.float32, attn_scale=0.3)
+    torch.cuda.synchronize()
+    q_rot = (query.double().numpy() @ rot.astype(np.float64)).astype(np.float32)
+    mid = native.stage1(q_rot, w.kv_cache, w.block_table, w.seq_lens, w.centroids, 16, num_kv_heads=8,
+                        attn_scale=0.3)
+    ro, rl = native.stage2(mid, w.seq_lens)
+    err_o, err_l = np.abs(out.cpu().numpy() - ro).max(), np.abs(lse.cpu().numpy() - rl).max()
+    print(f"batch {batch}: out max-abs {err_o:.3e}, lse max-abs {err_l:.3e}")
+    assert err_o <= 2e-4 and err_l <= 2e-4
