@@ -278,3 +278,41 @@ def test_store_then_decode_against_unquantized_attention(dev, layout, rotation):
     assert np.isfinite(out.cpu().numpy()).all() and np.isfinite(lse.cpu().numpy()).all()
     assert eo.max() <= 2 * 0.018739756 and eo.mean() <= 2 * 0.0028449418
     assert el.max() <= 2 * 0.0064659119 and el.mean() <= 2 * 0.0024851561
+
+
+@pytest.mark.parametrize("layout", ["soa", "aos"])
+def test_store_without_norm_correction(dev, layout):
+    """``norm_correction=False`` stores ``fp16(||k||)`` as the K scalar (``reference/soa_store.py``
+    without NORM_CORRECTION) and changes nothing else: the same inputs written with and without
+    it differ only in the K scalars, which then match ||k|| within one fp16 ulp."""
+    n_tok, n_blocks = 300, 24
+    key, value, slots, rot_t, cents, mids = make_inputs(17, n_tok, n_blocks, "bf16")
+    cache0 = np.zeros((n_blocks, BS, HK, 134), dtype=np.uint8)
+    with_nc = gpu_store(dev, key, value, slots, rot_t, cents, mids, cache0, "bf16", layout, True)
+    raw = gpu_store(dev, key, value, slots, rot_t, cents, mids, cache0, "bf16", layout, False)
+    keep = np.nonzero(slots >= 0)[0]
+    blocks, offs = slots[keep] // BS, slots[keep] % BS
+    gather = OL.gather_aos if layout == "aos" else OL.gather_soa
+    norm = np.sqrt((key[keep].astype(np.float64) ** 2).sum(-1))
+    for h in range(HK):
+        ak, an, av, as_, az = gather(with_nc, blocks, offs, h, BS, HK, D)
+        bk, bn, bv, bs_, bz = gather(raw, blocks, offs, h, BS, HK, D)
+        assert np.array_equal(ak, bk) and np.array_equal(av, bv)
+        assert np.array_equal(as_, bs_) and np.array_equal(az, bz)
+    scal = np.zeros(cache0.size, dtype=bool)
+    stride = BS * HK * 134
+    for blk, off in zip(blocks.astype(np.int64), offs.astype(np.int64)):
+        for h in range(HK):
+            b0 = (blk * stride + (off * HK + h) * 134 + 64 if layout == "aos"
+                  else blk * stride + BS * HK * 128 + (h * 3 * BS + off) * 2)
+            scal[b0:b0 + 2] = True
+    assert np.array_equal(with_nc.reshape(-1)[~scal], raw.reshape(-1)[~scal]), "bytes other than the K scalar differ"
+    stored = raw.reshape(-1)[scal].view(np.float16).astype(np.float64)
+    want = []
+    for i, (blk, off) in enumerate(zip(blocks.astype(np.int64), offs.astype(np.int64))):
+        for h in range(HK):
+            b0 = (blk * stride + (off * HK + h) * 134 + 64 if layout == "aos"
+                  else blk * stride + BS * HK * 128 + (h * 3 * BS + off) * 2)
+            want.append((b0, norm[i, h]))
+    want = np.array([v for _, v in sorted(want)])  # in byte order, as `stored`
+    assert np.all(np.abs(stored - want) <= np.abs(want) * 2.0 ** -10), "K scalar is not fp16(||k||)"
